@@ -1,0 +1,105 @@
+// common.hpp -- shared device helpers and host error plumbing for the gfx950
+// paged-attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/genllm_paged.h"
+
+namespace genllm {
+
+constexpr int kPage = GENLLM_PAGE_BLOCK_SIZE;  // tokens per page
+constexpr int kWave = 64;                      // CDNA wavefront
+
+// ------------------------------------------------------------------ errors
+// Thread-local message for genllm_last_error(); `fail` records and returns.
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+#define GENLLM_HIP_TRY(expr)                                   \
+    do {                                                       \
+        hipError_t _e = (expr);                                \
+        if (_e != hipSuccess) return ::genllm::hip_fail(_e, #expr); \
+    } while (0)
+
+// Launch status check (configuration errors show up immediately).
+#define GENLLM_LAUNCH_CHECK(name)                                       \
+    do {                                                                \
+        hipError_t _e = hipGetLastError();                              \
+        if (_e != hipSuccess) return ::genllm::hip_fail(_e, name " launch"); \
+    } while (0)
+
+// ------------------------------------------------------------------- bf16
+// bf16 -> fp32 is a 16-bit shift (include/utils/bfloat16.hpp:42-45).
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// fp32 -> bf16 exactly as bfloat16_t's constructor (bfloat16.hpp:18-41):
+// inf/NaN -> sign|0x7F80|(mantissa!=0), exponent 0 (zero, subnormal) -> signed
+// zero, else round to nearest even with carry (overflow reaches infinity).
+__device__ __forceinline__ uint32_t f32_to_bf16_ref(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t e = u & 0x7F800000u;
+    uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    uint32_t special = ((u >> 16) & 0x8000u) | 0x7F80u | ((u & 0x7FFFFFu) ? 1u : 0u);
+    uint32_t zero = (u >> 16) & 0x8000u;
+    return e == 0x7F800000u ? special : (e == 0u ? zero : rne);
+}
+// Truncating store of the CPU rms_norm's 8-wide part (normalization.cpp:25-31).
+__device__ __forceinline__ uint32_t f32_to_bf16_trunc(float f) { return __float_as_uint(f) >> 16; }
+
+__device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return (lo & 0xFFFFu) | (hi << 16); }
+
+// ----------------------------------------------------------- DPP reductions
+// Row (16-lane) butterflies with DPP: quad_perm [1,0,3,2], [2,3,0,1], then
+// half-row mirror and row mirror.  After the four steps every lane of the
+// 16-lane row holds the reduction over the row.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppRowMirror>(x));
+    return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp<kDppQuadXor1>(x);
+    x += dpp<kDppQuadXor2>(x);
+    x += dpp<kDppRowHalfMirror>(x);
+    x += dpp<kDppRowMirror>(x);
+    return x;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));  // MFMA A/B operand (8 bf16 per lane)
+typedef float f32x4_t __attribute__((ext_vector_type(4)));    // 16x16 MFMA C/D (4 fp32 per lane)
+
+// 16 bytes of bf16 bit patterns <-> MFMA operand
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8_t, u); }
+
+__device__ __forceinline__ f32x4_t mfma16x16x32(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Host helpers
+int device_cu_count();
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace genllm

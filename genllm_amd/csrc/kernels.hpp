@@ -1,0 +1,80 @@
+// kernels.hpp -- launch parameter blocks and launchers of the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace genllm {
+
+// Device page-table entries opened by this call, passed by value so that the
+// scatter needs no prior copy (decode opens at most one page per step).
+struct TableUpdate {
+    int32_t first = 0;
+    int32_t count = 0;
+    int32_t k[4] = {0, 0, 0, 0};
+    int32_t v[4] = {0, 0, 0, 0};
+};
+
+struct AppendParams {
+    const uint16_t* k = nullptr;
+    int64_t k_tok_stride = 0, k_head_stride = 0;
+    const uint16_t* v = nullptr;
+    int64_t v_tok_stride = 0, v_head_stride = 0;
+    const uint16_t* q = nullptr;
+    int64_t q_tok_stride = 0, q_head_stride = 0;
+    uint16_t* q_out = nullptr;
+    int64_t qo_tok_stride = 0, qo_head_stride = 0;
+    const float* gamma_k = nullptr;
+    const float* gamma_q = nullptr;
+    float eps = 0.0f;
+    const float* cos_tab = nullptr;
+    const float* sin_tab = nullptr;
+    int64_t rope_stride = 0;  // elements per table row
+    int64_t rope_pos0 = 0;
+    int32_t S = 0, Hkv = 0, Hq = 0;
+    int32_t pos0 = 0;         // cache position of token 0
+    int32_t nq_tasks = 0, nkv_tasks = 0;
+    uint16_t* k_pool = nullptr;
+    uint16_t* v_pool = nullptr;
+    int64_t page_elems = 0;   // 16 * Hkv * D
+    int32_t* k_ids = nullptr;
+    int32_t* v_ids = nullptr;
+    TableUpdate upd;
+};
+int launch_kv_append(const AppendParams& p, int head_dim, hipStream_t stream);
+
+struct AttnParams {
+    const uint16_t* q = nullptr;
+    int64_t q_head_stride = 0, q_tok_stride = 0;
+    uint16_t* out = nullptr;
+    int64_t o_head_stride = 0, o_tok_stride = 0;
+    const uint16_t* k_pool = nullptr;
+    const uint16_t* v_pool = nullptr;
+    const int32_t* k_ids = nullptr;
+    const int32_t* v_ids = nullptr;
+    int32_t n_pages = 0;      // pages holding tokens < n_cached
+    int32_t n_cached = 0;
+    int32_t S = 0, Hq = 0, Hkv = 0, G = 0;
+    float scale_log2 = 0.0f;  // scale * log2(e)
+    int32_t causal = 1;
+    int64_t page_elems = 0;
+    int64_t kv_row = 0;       // elements between consecutive tokens in a page (Hkv * D)
+    // split-K decode
+    float* partial = nullptr;
+    int32_t* counters = nullptr;
+    int32_t pages_per_split = 0, n_splits = 1, n_chunks = 1;
+};
+
+// Workspace layout of the split-K decode.
+size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages);
+int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws);
+int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream);
+int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream);
+
+int launch_rms_norm(uint16_t* out, const uint16_t* x, const float* w, int64_t rows, int hidden, float eps,
+                    hipStream_t stream);
+int launch_apply_rope(uint16_t* out, const uint16_t* x, const float* cos_tab, const float* sin_tab, int n_heads,
+                      int seq_len, int head_dim, int64_t start_pos, hipStream_t stream);
+
+}  // namespace genllm

@@ -1,0 +1,665 @@
+// kv_cache.hip -- host side of the path: the kv_cache memory pool, the
+// PagedAttentionManager / BlockPool state machine, and the C ABI entry points.
+//
+// Reference: include/core/page_attention.h:9-90, src/core/page_attention.cpp:25-216,
+// src/core/pools.cpp:17-48 (bump allocator), src/backend/cpu/attention.cpp:123-216
+// and src/backend/cuda/attention.cu:491-580 (the op).  Differences, by design:
+//   * the device page table lives in HBM next to the pools and is updated
+//     incrementally (the CUDA op mallocs, copies and frees it on every call);
+//   * the K/V append is one kernel (the CUDA path issues 2*S*Hkv memcpys);
+//   * a pool without free pages is an error that leaves the layer unchanged
+//     (the reference breaks out of the loop but still advances num_cached).
+#include <algorithm>
+#include <climits>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace genllm {
+
+// ------------------------------------------------------------------ errors
+static thread_local std::string t_error;
+void set_error(const std::string& msg) { t_error = msg; }
+int fail(int code, const std::string& msg) {
+    t_error = msg;
+    return code;
+}
+int hip_fail(hipError_t e, const char* what) {
+    return fail(GENLLM_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int device_cu_count() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+    return n;
+}
+
+// -------------------------------------------------------------- BlockPool
+// page_attention.h:11-45 / page_attention.cpp:25-64
+struct BlockPool {
+    int32_t capacity = 0;    // 0 = unbounded
+    int32_t num_blocks = 0;  // ids handed out so far (high-water mark)
+    std::vector<int32_t> free_list;
+
+    int32_t alloc() {
+        if (!free_list.empty()) {
+            const int32_t id = free_list.back();
+            free_list.pop_back();
+            return id;
+        }
+        if (capacity > 0 && num_blocks >= capacity) return -1;
+        return num_blocks++;
+    }
+    void free(int32_t id) {
+        if (id >= 0 && id < num_blocks) free_list.push_back(id);
+    }
+    void reset() {
+        free_list.clear();
+        for (int32_t i = 0; i < num_blocks; ++i) free_list.push_back(i);
+    }
+    int64_t available() const {
+        return int64_t(free_list.size()) + (capacity > 0 ? int64_t(capacity - num_blocks) : int64_t(INT32_MAX));
+    }
+};
+
+// page_attention.h:57-66 plus the device-side resources of the layer
+struct LayerState {
+    bool active = false;
+    int32_t num_cached = 0;
+    int32_t n_kv_heads = 0, head_dim = 0, dtype = 0;
+    BlockPool k_pool, v_pool;
+    std::vector<int32_t> k_ids, v_ids;  // page table
+    uint16_t* k_base = nullptr;
+    uint16_t* v_base = nullptr;
+    int32_t* d_k_ids = nullptr;
+    int32_t* d_v_ids = nullptr;
+    int32_t max_blocks = 0;
+    size_t block_bytes = 0;
+};
+
+}  // namespace genllm
+
+using namespace genllm;
+
+struct genllm_kv {
+    int32_t device = 0;
+    char* base = nullptr;  // kv_cache MemoryPool buffer
+    size_t capacity = 0, cursor = 0;
+    std::map<int32_t, LayerState> layers;
+    void* ws = nullptr;    // split-K decode workspace (zero-filled on allocation)
+    size_t ws_bytes = 0;
+};
+
+namespace {
+
+size_t elem_size(int32_t dtype) {
+    switch (dtype) {
+        case 0: return 4;   // F32
+        case 1: return 2;   // F16
+        case 30: return 2;  // BF16
+        default: return 0;
+    }
+}
+
+// MemoryPool::allocate (pools.cpp:17-48): aligned bump allocation.
+int pool_allocate(genllm_kv* kv, size_t size, size_t align, void** out) {
+    const size_t at = (kv->cursor + align - 1) & ~(align - 1);
+    if (at + size > kv->capacity)
+        return fail(GENLLM_ERR_NO_MEMORY, "kv_cache pool: out of memory, need " + std::to_string(size) +
+                                              " bytes, remaining " + std::to_string(kv->capacity - std::min(at, kv->capacity)));
+    *out = kv->base + at;
+    kv->cursor = at + size;
+    return GENLLM_OK;
+}
+
+int64_t pages_opened(int32_t num_cached, int32_t count) {
+    // positions g in [num_cached, num_cached+count) with g % 16 == 0
+    return (int64_t(num_cached) + count + kPage - 1) / kPage - (int64_t(num_cached) + kPage - 1) / kPage;
+}
+
+// append_kv_pages (page_attention.cpp:141-162) on the host state.  New entries
+// go to the device table either through `upd` (when given and small enough) or
+// with an async copy on `stream`.
+int append_pages(LayerState& s, int32_t count, hipStream_t stream, TableUpdate* upd) {
+    if (upd) *upd = TableUpdate{};
+    if (!s.active || count <= 0) return GENLLM_OK;
+    const int64_t need = pages_opened(s.num_cached, count);
+    if (need > s.k_pool.available() || need > s.v_pool.available())
+        return fail(GENLLM_ERR_POOL_FULL, "append_kv_pages: block pool exhausted (" + std::to_string(need) +
+                                              " pages needed)");
+    const size_t old_size = s.k_ids.size();
+    for (int32_t p = 0; p < count; ++p) {
+        const int32_t g = s.num_cached + p;
+        if (g % kPage == 0) {
+            const int32_t k = s.k_pool.alloc();
+            const int32_t v = s.v_pool.alloc();
+            if (g / kPage >= int32_t(s.k_ids.size())) {
+                s.k_ids.push_back(k);
+                s.v_ids.push_back(v);
+            }
+        }
+    }
+    s.num_cached += count;
+    const size_t new_size = s.k_ids.size();
+    if (new_size > old_size && s.d_k_ids) {
+        if (new_size > size_t(s.max_blocks))
+            return fail(GENLLM_ERR_POOL_FULL, "append_kv_pages: page table longer than max_blocks");
+        const size_t n = new_size - old_size;
+        if (upd && n <= 4) {
+            upd->first = int32_t(old_size);
+            upd->count = int32_t(n);
+            for (size_t i = 0; i < n; ++i) {
+                upd->k[i] = s.k_ids[old_size + i];
+                upd->v[i] = s.v_ids[old_size + i];
+            }
+        } else {
+            GENLLM_HIP_TRY(hipMemcpyAsync(s.d_k_ids + old_size, s.k_ids.data() + old_size, n * sizeof(int32_t),
+                                          hipMemcpyHostToDevice, stream));
+            GENLLM_HIP_TRY(hipMemcpyAsync(s.d_v_ids + old_size, s.v_ids.data() + old_size, n * sizeof(int32_t),
+                                          hipMemcpyHostToDevice, stream));
+        }
+    }
+    return GENLLM_OK;
+}
+
+LayerState* active_layer(genllm_kv* kv, int32_t layer) {
+    auto it = kv->layers.find(layer);
+    if (it == kv->layers.end() || !it->second.active) return nullptr;
+    return &it->second;
+}
+
+// Split-K workspace sized for the layer's max_blocks, grown when a wider query
+// chunk needs more rows; zero-filled because the kernel's counters start at 0.
+int ensure_workspace(genllm_kv* kv, size_t need) {
+    if (need <= kv->ws_bytes) return GENLLM_OK;
+    if (kv->ws) {
+        GENLLM_HIP_TRY(hipDeviceSynchronize());
+        GENLLM_HIP_TRY(hipFree(kv->ws));
+        kv->ws = nullptr;
+        kv->ws_bytes = 0;
+    }
+    GENLLM_HIP_TRY(hipMalloc(&kv->ws, need));
+    GENLLM_HIP_TRY(hipMemset(kv->ws, 0, need));
+    kv->ws_bytes = need;
+    return GENLLM_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int check_attn_args(const AttnParams& p, int head_dim) {
+    if (!p.q || !p.out || !p.k_pool || !p.v_pool || !p.k_ids || !p.v_ids)
+        return fail(GENLLM_ERR_INVALID, "paged attention: null pointer");
+    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged attention requires head_dim == 128");
+    if (p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv != 0)
+        return fail(GENLLM_ERR_INVALID, "paged attention: n_q_heads must be a multiple of n_kv_heads");
+    if (p.S <= 0 || p.n_cached < p.S || p.n_pages < (p.n_cached + kPage - 1) / kPage)
+        return fail(GENLLM_ERR_INVALID, "paged attention: need 0 < seq_len <= n_cached <= 16 * n_pages");
+    if (!aligned(p.q, 16) || !aligned(p.k_pool, 16) || !aligned(p.v_pool, 16) || !aligned(p.out, 8) ||
+        (p.q_head_stride % 8) || (p.q_tok_stride % 8) || (p.o_head_stride % 4) || (p.o_tok_stride % 4))
+        return fail(GENLLM_ERR_INVALID, "paged attention: q/pools must be 16-byte aligned, strides multiples of 8");
+    return GENLLM_OK;
+}
+
+// Short query chunks (<= 16 rows per kv head) take the split-K decode kernel,
+// with the manager's workspace sized for the layer's largest table (a split
+// holds at least 4 pages unless GENLLM_DECODE_PPS asks for fewer); longer
+// chunks take the MFMA prefill kernel.
+int run_attention(AttnParams p, int head_dim, int32_t max_blocks, hipStream_t stream, genllm_kv* kv) {
+    if (int rc = check_attn_args(p, head_dim)) return rc;
+    if (p.G * p.S <= 16) {
+        const int ws_pages = std::max(p.n_pages, max_blocks);
+        const size_t need = decode_workspace_bytes(p.Hq, p.Hkv, p.S, head_dim, std::max(1, (ws_pages + 3) / 4));
+        if (int rc = ensure_workspace(kv, need)) return rc;
+        if (int rc = decode_plan(p, head_dim, kv->ws_bytes, kv->ws)) return rc;
+        return launch_paged_decode(p, head_dim, stream);
+    }
+    return launch_paged_prefill(p, head_dim, stream);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" const char* genllm_last_error(void) { return t_error.c_str(); }
+
+extern "C" int genllm_kv_create(int32_t device, size_t kv_pool_bytes, genllm_kv** out) {
+    if (!out) return fail(GENLLM_ERR_INVALID, "kv_create: null out");
+    *out = nullptr;
+    GENLLM_HIP_TRY(hipSetDevice(device));
+    genllm_kv* kv = new genllm_kv;
+    kv->device = device;
+    kv->capacity = kv_pool_bytes;
+    if (kv_pool_bytes > 0) {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, kv_pool_bytes);
+        if (e != hipSuccess) {
+            delete kv;
+            return fail(GENLLM_ERR_NO_MEMORY, std::string("kv_create: hipMalloc failed: ") + hipGetErrorString(e));
+        }
+        // pools start zeroed, as the reference's CPU pools (resource_cpu.cpp:43)
+        e = hipMemset(p, 0, kv_pool_bytes);
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            delete kv;
+            return hip_fail(e, "kv_create: hipMemset");
+        }
+        kv->base = static_cast<char*>(p);
+    }
+    *out = kv;
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_destroy(genllm_kv* kv) {
+    if (!kv) return GENLLM_OK;
+    (void)hipSetDevice(kv->device);
+    (void)hipDeviceSynchronize();
+    if (kv->base) (void)hipFree(kv->base);
+    if (kv->ws) (void)hipFree(kv->ws);
+    delete kv;
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_init_layer(genllm_kv* kv, int32_t layer, int32_t n_kv_heads, int32_t head_dim,
+                                    int32_t dtype) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "init_layer: null kv");
+    if (n_kv_heads <= 0 || head_dim <= 0 || elem_size(dtype) == 0)
+        return fail(GENLLM_ERR_INVALID, "init_layer: bad n_kv_heads/head_dim/dtype");
+    LayerState& s = kv->layers[layer];
+    s.n_kv_heads = n_kv_heads;
+    s.head_dim = head_dim;
+    s.dtype = dtype;
+    s.active = true;
+    s.num_cached = 0;
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max_blocks) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "reserve_layer: null kv");
+    if (max_blocks <= 0) return fail(GENLLM_ERR_INVALID, "reserve_layer: max_blocks must be > 0");
+    LayerState& s = kv->layers[layer];
+    if (!s.active || !kv->base) return GENLLM_OK;  // page_attention.cpp:84
+    const size_t bb = size_t(kPage) * s.n_kv_heads * s.head_dim * elem_size(s.dtype);
+    const size_t total = size_t(max_blocks) * bb;
+    void *kp, *vp, *ki, *vi;
+    if (int rc = pool_allocate(kv, total, 256, &kp)) return rc;
+    if (int rc = pool_allocate(kv, total, 256, &vp)) return rc;
+    if (int rc = pool_allocate(kv, size_t(max_blocks) * 4, 256, &ki)) return rc;
+    if (int rc = pool_allocate(kv, size_t(max_blocks) * 4, 256, &vi)) return rc;
+    s.k_base = static_cast<uint16_t*>(kp);
+    s.v_base = static_cast<uint16_t*>(vp);
+    s.d_k_ids = static_cast<int32_t*>(ki);
+    s.d_v_ids = static_cast<int32_t*>(vi);
+    s.block_bytes = bb;
+    s.max_blocks = max_blocks;
+    s.k_pool = BlockPool{};
+    s.v_pool = BlockPool{};
+    s.k_pool.capacity = max_blocks;
+    s.v_pool.capacity = max_blocks;
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_is_active(genllm_kv* kv, int32_t layer, int32_t* active) {
+    if (!kv || !active) return fail(GENLLM_ERR_INVALID, "is_active: null pointer");
+    *active = active_layer(kv, layer) != nullptr;
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_append_pages(genllm_kv* kv, int32_t layer, int32_t count, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "append_pages: null kv");
+    LayerState& s = kv->layers[layer];
+    return append_pages(s, count, as_stream(stream), nullptr);
+}
+
+extern "C" int genllm_kv_reset(genllm_kv* kv) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "reset: null kv");
+    for (auto& [id, s] : kv->layers) {
+        s.num_cached = 0;
+        s.k_ids.clear();
+        s.v_ids.clear();
+        s.k_pool.reset();
+        s.v_pool.reset();
+    }
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_layer_info(genllm_kv* kv, int32_t layer, genllm_layer_info* out) {
+    if (!kv || !out) return fail(GENLLM_ERR_INVALID, "layer_info: null pointer");
+    std::memset(out, 0, sizeof *out);
+    auto it = kv->layers.find(layer);
+    if (it == kv->layers.end()) return GENLLM_OK;
+    const LayerState& s = it->second;
+    out->active = s.active;
+    out->num_cached = s.num_cached;
+    out->num_pages = int32_t(s.k_ids.size());
+    out->n_kv_heads = s.n_kv_heads;
+    out->head_dim = s.head_dim;
+    out->dtype = s.dtype;
+    out->max_blocks = s.max_blocks;
+    out->k_num_blocks = s.k_pool.num_blocks;
+    out->k_num_free = int32_t(s.k_pool.free_list.size());
+    out->v_num_blocks = s.v_pool.num_blocks;
+    out->v_num_free = int32_t(s.v_pool.free_list.size());
+    out->k_pool = s.k_base;
+    out->v_pool = s.v_base;
+    out->k_ids = s.d_k_ids;
+    out->v_ids = s.d_v_ids;
+    out->block_bytes = s.block_bytes;
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_page_table(genllm_kv* kv, int32_t layer, int32_t* k_ids, int32_t* v_ids, int32_t cap,
+                                    int32_t* n) {
+    if (!kv || !n) return fail(GENLLM_ERR_INVALID, "page_table: null pointer");
+    auto it = kv->layers.find(layer);
+    *n = 0;
+    if (it == kv->layers.end()) return GENLLM_OK;
+    const LayerState& s = it->second;
+    *n = int32_t(s.k_ids.size());
+    for (int32_t i = 0; i < *n && i < cap; ++i) {
+        if (k_ids) k_ids[i] = s.k_ids[i];
+        if (v_ids) v_ids[i] = s.v_ids[i];
+    }
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_set_page_table(genllm_kv* kv, int32_t layer, const int32_t* k_ids, const int32_t* v_ids,
+                                        int32_t n, int32_t num_cached, void* stream) {
+    if (!kv || (n > 0 && (!k_ids || !v_ids))) return fail(GENLLM_ERR_INVALID, "set_page_table: null pointer");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return fail(GENLLM_ERR_INVALID, "set_page_table: layer not active");
+    if (n < 0 || num_cached < 0 || (s->max_blocks > 0 && n > s->max_blocks) || int64_t(num_cached) > int64_t(n) * kPage)
+        return fail(GENLLM_ERR_INVALID, "set_page_table: bad length or num_cached");
+    for (int32_t i = 0; i < n; ++i)
+        if (k_ids[i] < 0 || k_ids[i] >= s->k_pool.num_blocks || v_ids[i] < 0 || v_ids[i] >= s->v_pool.num_blocks)
+            return fail(GENLLM_ERR_INVALID, "set_page_table: id was never handed out by its pool");
+    s->k_ids.assign(k_ids, k_ids + n);
+    s->v_ids.assign(v_ids, v_ids + n);
+    s->num_cached = num_cached;
+    if (n > 0 && s->d_k_ids) {
+        GENLLM_HIP_TRY(hipMemcpyAsync(s->d_k_ids, s->k_ids.data(), size_t(n) * 4, hipMemcpyHostToDevice,
+                                      as_stream(stream)));
+        GENLLM_HIP_TRY(hipMemcpyAsync(s->d_v_ids, s->v_ids.data(), size_t(n) * 4, hipMemcpyHostToDevice,
+                                      as_stream(stream)));
+        GENLLM_HIP_TRY(hipStreamSynchronize(as_stream(stream)));  // host vectors may be reassigned next
+    }
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_block_alloc(genllm_kv* kv, int32_t layer, int32_t which, int32_t* id) {
+    if (!kv || !id) return fail(GENLLM_ERR_INVALID, "block_alloc: null pointer");
+    LayerState& s = kv->layers[layer];
+    *id = (which ? s.v_pool : s.k_pool).alloc();
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_block_free(genllm_kv* kv, int32_t layer, int32_t which, int32_t id) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "block_free: null kv");
+    LayerState& s = kv->layers[layer];
+    (which ? s.v_pool : s.k_pool).free(id);
+    return GENLLM_OK;
+}
+
+// ------------------------------------------------------------------ the op
+extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* q, const void* k, const void* v,
+                                      void* out, int32_t batch, int32_t n_q_heads, int32_t seq_len,
+                                      int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups, float scale,
+                                      int32_t causal, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "paged_attention: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return GENLLM_OK;  // attention.cpp:127: inactive layer, nothing written
+    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention requires head_dim == 128");
+    if (batch != 1) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention: batch must be 1");
+    if (s->dtype != GENLLM_DTYPE_BF16 || s->head_dim != head_dim || s->n_kv_heads != n_kv_heads)
+        return fail(GENLLM_ERR_INVALID, "paged_attention: tensor shape/dtype differs from the layer's pools");
+    if (n_kv_groups <= 0 || n_q_heads != n_kv_heads * n_kv_groups)
+        return fail(GENLLM_ERR_INVALID, "paged_attention: n_q_heads must equal n_kv_heads * n_kv_groups");
+    if (!q || !k || !v || !out) return fail(GENLLM_ERR_INVALID, "paged_attention: null tensor");
+    if (!s->k_base) return fail(GENLLM_ERR_INVALID, "paged_attention: layer has no reserved pools");
+    if (seq_len <= 0) return GENLLM_OK;
+    if (!aligned(k, 16) || !aligned(v, 16))
+        return fail(GENLLM_ERR_INVALID, "paged_attention: k/v must be 16-byte aligned");
+    hipStream_t st = as_stream(stream);
+
+    // 1. append (append_kv_from_tensor, attention.cpp:146): head-major [Hkv][S][D]
+    const int32_t pos0 = s->num_cached;
+    AppendParams ap;
+    if (int rc = append_pages(*s, seq_len, st, &ap.upd)) return rc;
+    ap.k = static_cast<const uint16_t*>(k);
+    ap.v = static_cast<const uint16_t*>(v);
+    ap.k_tok_stride = ap.v_tok_stride = head_dim;
+    ap.k_head_stride = ap.v_head_stride = int64_t(seq_len) * head_dim;
+    ap.S = seq_len;
+    ap.Hkv = n_kv_heads;
+    ap.pos0 = pos0;
+    ap.nkv_tasks = (n_kv_heads + 7) / 8;
+    ap.k_pool = s->k_base;
+    ap.v_pool = s->v_base;
+    ap.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
+    ap.k_ids = s->d_k_ids;
+    ap.v_ids = s->d_v_ids;
+    if (int rc = launch_kv_append(ap, head_dim, st)) return rc;
+    if (s->k_ids.empty()) return GENLLM_OK;  // attention.cpp:148
+
+    // 2. attend over all cached tokens
+    AttnParams p;
+    p.q = static_cast<const uint16_t*>(q);
+    p.q_head_stride = int64_t(seq_len) * head_dim;
+    p.q_tok_stride = head_dim;
+    p.out = static_cast<uint16_t*>(out);
+    p.o_head_stride = int64_t(seq_len) * head_dim;
+    p.o_tok_stride = head_dim;
+    p.k_pool = s->k_base;
+    p.v_pool = s->v_base;
+    p.k_ids = s->d_k_ids;
+    p.v_ids = s->d_v_ids;
+    p.n_cached = s->num_cached;
+    p.n_pages = std::min<int32_t>(int32_t(s->k_ids.size()), (s->num_cached + kPage - 1) / kPage);
+    p.S = seq_len;
+    p.Hq = n_q_heads;
+    p.Hkv = n_kv_heads;
+    p.G = n_kv_groups;
+    p.scale_log2 = scale * kLog2e;
+    p.causal = causal != 0;
+    p.page_elems = ap.page_elems;
+    p.kv_row = int64_t(n_kv_heads) * head_dim;
+    return run_attention(p, head_dim, s->max_blocks, st, kv);
+}
+
+extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t seq_len, const void* k,
+                                          int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                                          int64_t v_tok_stride, int64_t v_head_stride, const float* gamma_k,
+                                          const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                          int32_t n_q_heads, const float* gamma_q, void* q_out,
+                                          int64_t qo_tok_stride, int64_t qo_head_stride, float eps,
+                                          const float* cos_tab, const float* sin_tab, int64_t rope_pos0,
+                                          void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return GENLLM_OK;
+    if (!s->k_base) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: layer has no reserved pools");
+    const int D = s->head_dim;
+    if (D != 64 && D != 128 && D != 256) return fail(GENLLM_ERR_UNSUPPORTED, "qk_norm_rope_append: head_dim");
+    if (s->dtype != GENLLM_DTYPE_BF16) return fail(GENLLM_ERR_UNSUPPORTED, "qk_norm_rope_append: bf16 only");
+    if (seq_len <= 0) return GENLLM_OK;
+    if (!k || !v) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: null k/v");
+    if ((cos_tab == nullptr) != (sin_tab == nullptr))
+        return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: cos and sin tables go together");
+    if (q && (!q_out || n_q_heads <= 0)) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: q needs q_out");
+    if (!aligned(k, 8) || !aligned(v, 16) || (k_tok_stride % 4) || (k_head_stride % 4) || (v_tok_stride % 8) ||
+        (v_head_stride % 8) || (q && (!aligned(q, 8) || !aligned(q_out, 8) || (q_tok_stride % 4) ||
+                                      (q_head_stride % 4) || (qo_tok_stride % 4) || (qo_head_stride % 4))) ||
+        (gamma_k && !aligned(gamma_k, 16)) || (gamma_q && !aligned(gamma_q, 16)) ||
+        (cos_tab && (!aligned(cos_tab, 16) || !aligned(sin_tab, 16))))
+        return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: misaligned pointer or stride");
+    hipStream_t st = as_stream(stream);
+    AppendParams ap;
+    const int32_t pos0 = s->num_cached;
+    if (int rc = append_pages(*s, seq_len, st, &ap.upd)) return rc;
+    ap.k = static_cast<const uint16_t*>(k);
+    ap.k_tok_stride = k_tok_stride;
+    ap.k_head_stride = k_head_stride;
+    ap.v = static_cast<const uint16_t*>(v);
+    ap.v_tok_stride = v_tok_stride;
+    ap.v_head_stride = v_head_stride;
+    ap.q = static_cast<const uint16_t*>(q);
+    ap.q_tok_stride = q_tok_stride;
+    ap.q_head_stride = q_head_stride;
+    ap.q_out = static_cast<uint16_t*>(q_out);
+    ap.qo_tok_stride = qo_tok_stride;
+    ap.qo_head_stride = qo_head_stride;
+    ap.gamma_k = gamma_k;
+    ap.gamma_q = gamma_q;
+    ap.eps = eps;
+    ap.cos_tab = cos_tab;
+    ap.sin_tab = sin_tab;
+    ap.rope_stride = D;
+    ap.rope_pos0 = rope_pos0;
+    ap.S = seq_len;
+    ap.Hkv = s->n_kv_heads;
+    ap.Hq = q ? n_q_heads : 0;
+    ap.pos0 = pos0;
+    ap.nq_tasks = q ? (n_q_heads + 7) / 8 : 0;
+    ap.nkv_tasks = (s->n_kv_heads + 7) / 8;
+    ap.k_pool = s->k_base;
+    ap.v_pool = s->v_base;
+    ap.page_elems = int64_t(kPage) * s->n_kv_heads * D;
+    ap.k_ids = s->d_k_ids;
+    ap.v_ids = s->d_v_ids;
+    return launch_kv_append(ap, D, st);
+}
+
+// ---------------------------------------------------------- stateless ops
+extern "C" int genllm_rms_norm(void* out, const void* x, const float* w, int64_t rows, int32_t hidden, float eps,
+                               void* stream) {
+    if (!out || !x || !w || hidden <= 0) return fail(GENLLM_ERR_INVALID, "rms_norm: bad arguments");
+    return launch_rms_norm(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(x), w, rows, hidden, eps,
+                           as_stream(stream));
+}
+
+extern "C" int genllm_apply_rope(void* out, const void* x, const float* cos_tab, const float* sin_tab,
+                                 int32_t n_heads, int32_t seq_len, int32_t head_dim, int64_t start_pos,
+                                 void* stream) {
+    if (!out || !x || !cos_tab || !sin_tab || head_dim <= 0 || head_dim % 2 || start_pos < 0)
+        return fail(GENLLM_ERR_INVALID, "apply_rope: bad arguments");
+    return launch_apply_rope(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(x), cos_tab, sin_tab,
+                             n_heads, seq_len, head_dim, start_pos, as_stream(stream));
+}
+
+extern "C" int genllm_rope_cache(float* dst, float theta, int32_t head_dim, int32_t max_seq, int32_t is_cos) {
+    // RopeCacheImpl<CPU> (rope.cpp:121-148): double-precision angles, each value
+    // stored at i and i + head_dim/2.
+    if (!dst || head_dim <= 0 || head_dim % 2 || max_seq < 0) return fail(GENLLM_ERR_INVALID, "rope_cache: bad args");
+    const int half = head_dim / 2;
+    std::vector<double> inv(half);
+    for (int i = 0; i < half; ++i) inv[i] = 1.0 / std::pow(double(theta), (2.0 * double(i)) / double(head_dim));
+    for (int s = 0; s < max_seq; ++s) {
+        for (int i = 0; i < half; ++i) {
+            const double a = double(s) * inv[i];
+            const float val = is_cos ? float(std::cos(a)) : float(std::sin(a));
+            dst[size_t(s) * head_dim + i] = val;
+            dst[size_t(s) * head_dim + i + half] = val;
+        }
+    }
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_scatter(const void* k, int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                                 int64_t v_tok_stride, int64_t v_head_stride, void* k_pool, void* v_pool,
+                                 const int32_t* k_ids, const int32_t* v_ids, int32_t pos0, int32_t seq_len,
+                                 int32_t n_kv_heads, int32_t head_dim, void* stream) {
+    if (!k || !v || !k_pool || !v_pool || !k_ids || !v_ids || n_kv_heads <= 0 || pos0 < 0)
+        return fail(GENLLM_ERR_INVALID, "kv_scatter: bad arguments");
+    if (!aligned(k, 8) || !aligned(v, 16) || (k_tok_stride % 4) || (k_head_stride % 4) || (v_tok_stride % 8) ||
+        (v_head_stride % 8))
+        return fail(GENLLM_ERR_INVALID, "kv_scatter: misaligned pointer or stride");
+    AppendParams ap;
+    ap.k = static_cast<const uint16_t*>(k);
+    ap.k_tok_stride = k_tok_stride;
+    ap.k_head_stride = k_head_stride;
+    ap.v = static_cast<const uint16_t*>(v);
+    ap.v_tok_stride = v_tok_stride;
+    ap.v_head_stride = v_head_stride;
+    ap.S = seq_len;
+    ap.Hkv = n_kv_heads;
+    ap.pos0 = pos0;
+    ap.nkv_tasks = (n_kv_heads + 7) / 8;
+    ap.k_pool = static_cast<uint16_t*>(k_pool);
+    ap.v_pool = static_cast<uint16_t*>(v_pool);
+    ap.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
+    ap.k_ids = const_cast<int32_t*>(k_ids);
+    ap.v_ids = const_cast<int32_t*>(v_ids);
+    return launch_kv_append(ap, head_dim, as_stream(stream));
+}
+
+extern "C" size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int32_t seq_len,
+                                                      int32_t head_dim, int32_t max_pages) {
+    return decode_workspace_bytes(n_q_heads, n_kv_heads, seq_len, head_dim, max_pages);
+}
+
+static AttnParams make_attn(const void* q, int64_t q_head_stride, int64_t q_tok_stride, void* out,
+                            int64_t o_head_stride, int64_t o_tok_stride, const void* k_pool, const void* v_pool,
+                            const int32_t* k_ids, const int32_t* v_ids, int32_t n_pages, int32_t n_cached,
+                            int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                            int32_t causal) {
+    AttnParams p;
+    p.q = static_cast<const uint16_t*>(q);
+    p.q_head_stride = q_head_stride;
+    p.q_tok_stride = q_tok_stride;
+    p.out = static_cast<uint16_t*>(out);
+    p.o_head_stride = o_head_stride;
+    p.o_tok_stride = o_tok_stride;
+    p.k_pool = static_cast<const uint16_t*>(k_pool);
+    p.v_pool = static_cast<const uint16_t*>(v_pool);
+    p.k_ids = k_ids;
+    p.v_ids = v_ids;
+    p.n_pages = std::min(n_pages, (n_cached + kPage - 1) / kPage);
+    p.n_cached = n_cached;
+    p.S = seq_len;
+    p.Hq = n_q_heads;
+    p.Hkv = n_kv_heads;
+    p.G = n_kv_heads > 0 ? n_q_heads / n_kv_heads : 0;
+    p.scale_log2 = scale * kLog2e;
+    p.causal = causal != 0;
+    p.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
+    p.kv_row = int64_t(n_kv_heads) * head_dim;
+    return p;
+}
+
+extern "C" int genllm_paged_decode(const void* q, int64_t q_head_stride, int64_t q_tok_stride, void* out,
+                                   int64_t o_head_stride, int64_t o_tok_stride, const void* k_pool,
+                                   const void* v_pool, const int32_t* k_ids, const int32_t* v_ids, int32_t n_pages,
+                                   int32_t n_cached, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, float scale, int32_t causal, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    AttnParams p = make_attn(q, q_head_stride, q_tok_stride, out, o_head_stride, o_tok_stride, k_pool, v_pool, k_ids,
+                             v_ids, n_pages, n_cached, seq_len, n_q_heads, n_kv_heads, head_dim, scale, causal);
+    if (int rc = check_attn_args(p, head_dim)) return rc;
+    if (p.G * p.S > 16)
+        return fail(GENLLM_ERR_INVALID, "paged_decode: seq_len * groups must be <= 16 (use paged_prefill)");
+    if (int rc = decode_plan(p, head_dim, workspace_bytes, workspace)) return rc;
+    return launch_paged_decode(p, head_dim, as_stream(stream));
+}
+
+extern "C" int genllm_paged_prefill(const void* q, int64_t q_head_stride, int64_t q_tok_stride, void* out,
+                                    int64_t o_head_stride, int64_t o_tok_stride, const void* k_pool,
+                                    const void* v_pool, const int32_t* k_ids, const int32_t* v_ids, int32_t n_pages,
+                                    int32_t n_cached, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, float scale, int32_t causal, void* stream) {
+    AttnParams p = make_attn(q, q_head_stride, q_tok_stride, out, o_head_stride, o_tok_stride, k_pool, v_pool, k_ids,
+                             v_ids, n_pages, n_cached, seq_len, n_q_heads, n_kv_heads, head_dim, scale, causal);
+    if (int rc = check_attn_args(p, head_dim)) return rc;
+    return launch_paged_prefill(p, head_dim, as_stream(stream));
+}

@@ -1,0 +1,252 @@
+// paged_prefill.hip -- causal paged FlashAttention on bf16 MFMA (gfx950).
+//
+// Same result as the attention loop of PagedAttentionImpl<CPU>::execute
+// (src/backend/cpu/attention.cpp:148-215) for a chunk of S queries: query s sits
+// at q_abs = n_cached - S + s and attends keys 0..q_abs (causal, :164-181),
+// kv head = q head / groups (:158).
+//
+// Grid (query tiles, Hq), WAVES x 64 threads.  A workgroup owns QW*WAVES
+// consecutive queries of one q head; wave w owns 32 of them (two 16-row
+// MFMA blocks).  K/V tiles of 64 tokens (4 pages) are gathered through the
+// block table into LDS:
+//   K  as [token][dim]  (row pad 16 B),
+//   V  transposed as [dim][token] (row pad 8 B) -- pairs of tokens are packed
+//      into dwords so the transpose is plain ds_write_b32.
+// Per tile and wave, with v_mfma_f32_16x16x32_bf16:
+//   S^T = K Q^T  (A = K from LDS: lane l -> token l%16 of a 16-block, dims
+//        32ks+8(l/16)..; B = Q^T held in registers).  D[tok][q] lands in lane
+//        q%16 + 16*(tok%16/4), register tok%4: every lane holds 16 keys of ONE
+//        query row per 16-query block, so the online softmax state (m, l) of a
+//        row is per lane and the row max needs only two cross-lane shuffles.
+//   O^T += V^T P^T  (A = V^T from LDS, two 8-byte reads; B = P^T taken from the
+//        lane's own S^T registers after exp2 and bf16 packing -- the 8 keys of
+//        lane group g for k-step kt are {32kt+4g+i, 32kt+16+4g+i}, i<4, and
+//        the V^T reads use the same 8 keys).  O^T[dim][q] again belongs to the
+//        lane's own query, so the rescale by 2^(m_old-m_new) is lane-local.
+// Heaviest query tiles are launched first (causal work grows with the tile).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace genllm {
+
+namespace {
+
+constexpr int KT = 64;  // keys per tile (4 pages)
+constexpr int QW = 32;  // queries per wave
+
+__device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
+    const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
+    return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+template <int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p) {
+    static_assert(D == 128, "prefill kernel: head_dim 128");
+    constexpr int KS = D / 32;     // k-steps of the S^T product
+    constexpr int DB = D / 16;     // 16-dim blocks of O^T
+    constexpr int KROW = D + 8;    // K tile row stride (elements)
+    constexpr int VROW = KT + 4;   // V^T tile row stride (elements)
+    constexpr int NT = WAVES * 64;
+    constexpr int QT = QW * WAVES;
+
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[KT * KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * VROW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int n_qt = (p.S + QT - 1) / QT;
+    const int qt = n_qt - 1 - int(blockIdx.x);
+    const int hq = blockIdx.y;
+    const int hkv = hq / p.G;
+    const int qabs0 = p.n_cached - p.S;   // absolute position of query 0
+    const int q0 = qt * QT + wv * QW;     // first query of this wave
+
+    // Q^T operands (B): lane -> query q0 + 16nb + n16, dims 32ks + 8g..+7
+    bf16x8_t qb[2][KS];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int s = q0 + 16 * nb + n16;
+        const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(s) * p.q_tok_stride;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            uint4 u = make_uint4(0, 0, 0, 0);
+            if (s < p.S) u = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
+            qb[nb][ks] = as_bf16x8(u);
+        }
+    }
+
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    f32x4_t acc[DB][2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[db][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int wg_last = min(qt * QT + QT, p.S) - 1;
+    const int kv_end = p.causal ? min(qabs0 + wg_last + 1, p.n_cached) : p.n_cached;
+    const int n_tiles = (kv_end + KT - 1) / KT;
+    const bool wave_has_rows = q0 < p.S;
+    const int w_last_abs = qabs0 + min(q0 + QW, p.S) - 1;
+    const int w_first_abs = qabs0 + q0;
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int tok0 = t * KT;
+        __syncthreads();
+        // ---- K tile: 64 tokens x D dims, 16-byte chunks
+        for (int c = tid; c < KT * (D / 8); c += NT) {
+            const int tt = c / (D / 8), ch = c - tt * (D / 8);
+            const int pos = tok0 + tt;
+            uint4 u = make_uint4(0, 0, 0, 0);
+            if (pos < p.n_cached) {
+                const int64_t id = p.k_ids[pos / kPage];
+                u = *reinterpret_cast<const uint4*>(p.k_pool + id * p.page_elems + int64_t(pos % kPage) * p.kv_row +
+                                                    hkv * D + 8 * ch);
+            }
+            *reinterpret_cast<uint4*>(&k_lds[tt * KROW + 8 * ch]) = u;
+        }
+        // ---- V tile, transposed: task = (token pair tp, 8-dim chunk ch)
+        for (int c = tid; c < (KT / 2) * (D / 8); c += NT) {
+            const int tp = c & (KT / 2 - 1), ch = c / (KT / 2);
+            const int pos = tok0 + 2 * tp;
+            uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+            if (pos < p.n_cached) {
+                const int64_t id = p.v_ids[pos / kPage];
+                a = *reinterpret_cast<const uint4*>(p.v_pool + id * p.page_elems + int64_t(pos % kPage) * p.kv_row +
+                                                    hkv * D + 8 * ch);
+            }
+            if (pos + 1 < p.n_cached) {
+                const int64_t id = p.v_ids[(pos + 1) / kPage];
+                b = *reinterpret_cast<const uint4*>(p.v_pool + id * p.page_elems +
+                                                    int64_t((pos + 1) % kPage) * p.kv_row + hkv * D + 8 * ch);
+            }
+            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t* row0 = reinterpret_cast<uint32_t*>(&v_lds[(8 * ch + 2 * e) * VROW + 2 * tp]);
+                uint32_t* row1 = reinterpret_cast<uint32_t*>(&v_lds[(8 * ch + 2 * e + 1) * VROW + 2 * tp]);
+                *row0 = (av[e] & 0xFFFFu) | (bv[e] << 16);
+                *row1 = (av[e] >> 16) | (bv[e] & 0xFFFF0000u);
+            }
+        }
+        __syncthreads();
+        if (!wave_has_rows || (p.causal && tok0 > w_last_abs)) continue;
+
+        // ---- S^T = K Q^T
+        f32x4_t s[4][2];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) s[mb][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const bf16x8_t a =
+                    as_bf16x8(*reinterpret_cast<const uint4*>(&k_lds[(16 * mb + n16) * KROW + 32 * ks + 8 * g]));
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) s[mb][nb] = mfma16x16x32(a, qb[nb][ks], s[mb][nb]);
+            }
+
+        // ---- online softmax, per lane = per query row
+        const bool need_mask = (p.causal && tok0 + KT - 1 > w_first_abs) || tok0 + KT > p.n_cached;
+        float alpha[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int qpos = qabs0 + q0 + 16 * nb + n16;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = s[mb][nb][i] * p.scale_log2;
+                    if (need_mask) {
+                        const int kpos = tok0 + 16 * mb + 4 * g + i;
+                        if (kpos >= p.n_cached || (p.causal && kpos > qpos)) v = -INFINITY;
+                    }
+                    s[mb][nb][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m[nb], mx);
+            const float mu = mn == -INFINITY ? 0.0f : mn;
+            alpha[nb] = exp2_fast(m[nb] - mu);
+            float sum = 0.0f;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = exp2_fast(s[mb][nb][i] - mu);
+                    s[mb][nb][i] = e;
+                    sum += e;
+                }
+            l[nb] = l[nb] * alpha[nb] + sum;
+            m[nb] = mn;
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) acc[db][nb] *= alpha[nb];
+
+        // ---- O^T += V^T P^T
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            bf16x8_t pb[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const f32x4_t& x0 = s[2 * kt][nb];
+                const f32x4_t& x1 = s[2 * kt + 1][nb];
+                uint4 u;
+                u.x = bf16_pair_rne(x0[0], x0[1]);
+                u.y = bf16_pair_rne(x0[2], x0[3]);
+                u.z = bf16_pair_rne(x1[0], x1[1]);
+                u.w = bf16_pair_rne(x1[2], x1[3]);
+                pb[nb] = as_bf16x8(u);
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const uint16_t* vr = &v_lds[(16 * db + n16) * VROW + 32 * kt + 4 * g];
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+                const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) acc[db][nb] = mfma16x16x32(a, pb[nb], acc[db][nb]);
+            }
+        }
+    }
+
+    if (!wave_has_rows) return;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        float lt = l[nb];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const float inv = 1.0f / lt;
+        const int s = q0 + 16 * nb + n16;
+        if (s >= p.S) continue;
+        uint16_t* orow = p.out + int64_t(hq) * p.o_head_stride + int64_t(s) * p.o_tok_stride;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const f32x4_t& a = acc[db][nb];
+            uint2 w;
+            w.x = pack2(f32_to_bf16_ref(a[0] * inv), f32_to_bf16_ref(a[1] * inv));
+            w.y = pack2(f32_to_bf16_ref(a[2] * inv), f32_to_bf16_ref(a[3] * inv));
+            *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = w;
+        }
+    }
+}
+
+}  // namespace
+
+int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream) {
+    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged prefill: head_dim must be 128");
+    if (p.S <= 0 || p.n_pages <= 0) return GENLLM_OK;
+    constexpr int WAVES = 4;
+    const int n_qt = (p.S + QW * WAVES - 1) / (QW * WAVES);
+    dim3 grid(n_qt, p.Hq);
+    hipLaunchKernelGGL((paged_prefill_kernel<128, WAVES>), grid, dim3(WAVES * 64), 0, stream, p);
+    GENLLM_LAUNCH_CHECK("paged_prefill_kernel");
+    return GENLLM_OK;
+}
+
+}  // namespace genllm

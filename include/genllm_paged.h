@@ -1,0 +1,201 @@
+/*
+ * genllm_paged.h -- C ABI of the MI355X (gfx950) paged KV-cache attention path.
+ *
+ * This is the drop-in boundary for Genllm's paged attention: a
+ * PagedAttentionImpl<Device::HIP> specialisation (same shape as
+ * include/backend/cpu/attention.h:15-18 in the reference) calls these
+ * functions with raw device pointers.  Plain C types only: pointers, sizes,
+ * int32/int64/float; `stream` is a hipStream_t passed as void* (NULL = the
+ * default stream).  Every function returns GENLLM_OK (0) or an error code, and
+ * genllm_last_error() describes the last failure of the calling thread.
+ *
+ * Not thread-safe per genllm_kv object (the reference's PagedAttentionManager
+ * is not either).  No call synchronises the stream; work is stream-ordered.
+ * Tensors are bf16 (GGML_TYPE_BF16 = 30) unless stated; gammas and RoPE tables
+ * are fp32, as in the reference.
+ */
+#ifndef GENLLM_PAGED_H
+#define GENLLM_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+#define GENLLM_OK 0
+#define GENLLM_ERR_INVALID 1     /* bad argument: null pointer, shape, layer state */
+#define GENLLM_ERR_UNSUPPORTED 2 /* head_dim / dtype the kernels do not cover
+                                    (reference throws, src/backend/cuda/attention.cu:511) */
+#define GENLLM_ERR_NO_MEMORY 3   /* kv_cache MemoryPool exhausted (reference throws,
+                                    src/core/pools.cpp:26-31) */
+#define GENLLM_ERR_POOL_FULL 4   /* BlockPool has no free page; the reference silently
+                                    truncates (src/core/page_attention.cpp:155,161) */
+#define GENLLM_ERR_HIP 5         /* HIP runtime error (allocation, copy, launch) */
+
+#define GENLLM_PAGE_BLOCK_SIZE 16 /* include/core/page_attention.h:9 */
+#define GENLLM_DTYPE_BF16 30      /* DataType::GGML_TYPE_BF16, include/utils/utils.hpp:59 */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *genllm_last_error(void);
+
+/* ------------------------------------------------------------- KV cache
+ * One genllm_kv = the device's kv_cache MemoryPool (include/core/pools.h:11-48,
+ * one hipMalloc of kv_pool_bytes, bump-allocated) plus the
+ * PagedAttentionManager living on it (include/core/page_attention.h:52-90):
+ * per layer a K and a V BlockPool of 16-token pages laid out [16][Hkv][D], a
+ * host page table of {k_block_id, v_block_id} and its device-resident copy.
+ */
+typedef struct genllm_kv genllm_kv;
+
+/* MemoryPool(kv_cache) + MemoryManager::create_attention_manager
+ * (src/core/pools.cpp:3-15, src/core/manager.cpp:102-116). */
+int genllm_kv_create(int32_t device, size_t kv_pool_bytes, genllm_kv **out);
+int genllm_kv_destroy(genllm_kv *kv);
+
+/* PagedAttentionManager::init_layer, src/core/page_attention.cpp:72-79 */
+int genllm_kv_init_layer(genllm_kv *kv, int32_t layer, int32_t n_kv_heads, int32_t head_dim, int32_t dtype);
+/* PagedAttentionManager::reserve_layer, page_attention.cpp:81-101: carves the
+ * K pool, the V pool and the device page table (max_blocks entries) from the
+ * kv_cache pool. */
+int genllm_kv_reserve_layer(genllm_kv *kv, int32_t layer, int32_t max_blocks);
+/* PagedAttentionManager::is_active, page_attention.h:82-85; *active = 0/1 */
+int genllm_kv_is_active(genllm_kv *kv, int32_t layer, int32_t *active);
+/* PagedAttentionManager::append_kv_pages, page_attention.cpp:141-162, plus the
+ * upload of the new table entries on `stream`.  Unlike the reference, a pool
+ * without enough free pages returns GENLLM_ERR_POOL_FULL and leaves the layer
+ * unchanged. */
+int genllm_kv_append_pages(genllm_kv *kv, int32_t layer, int32_t count, void *stream);
+/* PagedAttentionManager::reset (page_attention.cpp:208-216), reached through
+ * MemoryManager::reset_kv_cache (manager.cpp:97-101). Host-only. */
+int genllm_kv_reset(genllm_kv *kv);
+
+/* LayerState (page_attention.h:57-66) as plain fields. */
+typedef struct genllm_layer_info {
+    int32_t active;
+    int32_t num_cached;
+    int32_t num_pages;  /* page_table.size() */
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t dtype;
+    int32_t max_blocks; /* BlockPool capacity */
+    int32_t k_num_blocks, k_num_free, v_num_blocks, v_num_free;
+    void *k_pool;       /* device: K pool base (block 0) */
+    void *v_pool;       /* device: V pool base */
+    int32_t *k_ids;     /* device: page table, K block ids [max_blocks] */
+    int32_t *v_ids;     /* device: page table, V block ids [max_blocks] */
+    size_t block_bytes; /* 16 * n_kv_heads * head_dim * elem */
+} genllm_layer_info;
+int genllm_kv_layer_info(genllm_kv *kv, int32_t layer, genllm_layer_info *out);
+
+/* Copy of the host page table (LayerState::page_table); *n = its length. */
+int genllm_kv_page_table(genllm_kv *kv, int32_t layer, int32_t *k_ids, int32_t *v_ids, int32_t cap,
+                         int32_t *n);
+/* Direct mutation of the layer state (get_layer returns a mutable reference,
+ * page_attention.cpp:204-206): replaces the table and num_cached, uploads the
+ * table on `stream`.  Every id must be a block its pool has handed out. */
+int genllm_kv_set_page_table(genllm_kv *kv, int32_t layer, const int32_t *k_ids, const int32_t *v_ids,
+                             int32_t n, int32_t num_cached, void *stream);
+/* BlockPool::alloc / free / num_blocks / num_free (page_attention.cpp:37-57);
+ * which = 0 for the K pool, 1 for the V pool.  alloc writes -1 when full. */
+int genllm_kv_block_alloc(genllm_kv *kv, int32_t layer, int32_t which, int32_t *id);
+int genllm_kv_block_free(genllm_kv *kv, int32_t layer, int32_t which, int32_t id);
+
+/* ---------------------------------------------------------------- the op
+ * PagedAttentionImpl<D>::execute (src/backend/cpu/attention.cpp:123-216,
+ * src/backend/cuda/attention.cu:491-580): append this step's K/V to the layer's
+ * pages, then attend.  q, out: head-major [batch=1][n_q_heads][seq_len][head_dim];
+ * k, v: [1][n_kv_heads][seq_len][head_dim] (op_factory.hpp:413-476).  scale,
+ * causal and n_kv_groups are op_params[1..3].  An inactive layer returns
+ * GENLLM_OK without touching out (attention.cpp:127).  head_dim != 128 returns
+ * GENLLM_ERR_UNSUPPORTED (attention.cu:511).  seq_len == 1 runs the split-K
+ * decode kernel, longer chunks the MFMA prefill kernel. */
+int genllm_paged_attention(genllm_kv *kv, int32_t layer, const void *q, const void *k, const void *v, void *out,
+                           int32_t batch, int32_t n_q_heads, int32_t seq_len, int32_t head_dim,
+                           int32_t n_kv_heads, int32_t n_kv_groups, float scale, int32_t causal, void *stream);
+
+/* The Qwen3 layer's q/k per-head RMSNorm -> RoPE -> page scatter, fused
+ * (src/model/Qwen3.cpp:137-166 = RmsNormImpl normalization.cpp:138-153, then
+ * ApplyRopeImpl rope.cpp:76-119, then append_kv_from_tensor
+ * page_attention.cpp:104-140), as one kernel.  Appends seq_len tokens at the
+ * layer's num_cached; RoPE position of token t is rope_pos0 + t (op_params[2]).
+ * k, v: token-major [seq_len][n_kv_heads][head_dim] (pre-permute), strides in
+ * elements.  q (optional, NULL to skip) has its own strides and is written,
+ * normed and rotated, to q_out.  gamma_k/gamma_q may be NULL (no norm);
+ * cos_tab/sin_tab may be NULL (no RoPE); tables are [max_seq][head_dim] fp32
+ * as RopeCacheImpl builds them. */
+int genllm_qk_norm_rope_append(genllm_kv *kv, int32_t layer, int32_t seq_len,
+                               const void *k, int64_t k_tok_stride, int64_t k_head_stride,
+                               const void *v, int64_t v_tok_stride, int64_t v_head_stride,
+                               const float *gamma_k, const void *q, int64_t q_tok_stride, int64_t q_head_stride,
+                               int32_t n_q_heads, const float *gamma_q, void *q_out, int64_t qo_tok_stride,
+                               int64_t qo_head_stride, float eps, const float *cos_tab, const float *sin_tab,
+                               int64_t rope_pos0, void *stream);
+
+/* --------------------------------------------------- stateless kernels */
+
+/* RmsNormImpl<D>::execute (normalization.cpp:138-153 / rms_norm :44-107):
+ * rows x hidden bf16, fp32 gamma; same fp32 summation order and stores
+ * (truncation for whole 8-blocks, RNE for the tail) as the CPU op. */
+int genllm_rms_norm(void *out, const void *x, const float *w, int64_t rows, int32_t hidden, float eps,
+                    void *stream);
+/* ApplyRopeImpl<D>::execute (rope.cpp:76-119): head-major [n_heads][seq_len][head_dim]
+ * bf16, positions start_pos + s. */
+int genllm_apply_rope(void *out, const void *x, const float *cos_tab, const float *sin_tab, int32_t n_heads,
+                      int32_t seq_len, int32_t head_dim, int64_t start_pos, void *stream);
+/* RopeCacheImpl<CPU>::execute (rope.cpp:121-148) into host memory, in double
+ * precision like the reference; the caller copies it to the device once. */
+int genllm_rope_cache(float *host_dst, float theta, int32_t head_dim, int32_t max_seq, int32_t is_cos);
+
+/* Page scatter of append_kv_from_tensor (page_attention.cpp:104-140) without
+ * norm/RoPE: rows of token t (global position pos0 + t) go to page
+ * k_ids[(pos0+t)/16], slot (pos0+t)%16.  Strides in elements. */
+int genllm_kv_scatter(const void *k, int64_t k_tok_stride, int64_t k_head_stride, const void *v,
+                      int64_t v_tok_stride, int64_t v_head_stride, void *k_pool, void *v_pool,
+                      const int32_t *k_ids, const int32_t *v_ids, int32_t pos0, int32_t seq_len,
+                      int32_t n_kv_heads, int32_t head_dim, void *stream);
+
+/* Workspace for genllm_paged_decode: fp32 partial (m, l, o) per split plus one
+ * counter per (kv head, row chunk).  Must be zero-filled once before first use;
+ * the kernel leaves its counters at zero.  Two launches sharing a workspace
+ * must be ordered (same stream). */
+size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int32_t seq_len,
+                                           int32_t head_dim, int32_t max_pages);
+
+/* The attention loop of PagedAttentionImpl (attention.cpp:148-215) for short
+ * query chunks (seq_len * n_q_heads / n_kv_heads <= 16 rows per kv head):
+ * split-K over pages, GQA rows packed per kv head, LSE merge of the splits in
+ * the same launch.  q/out rows addressed as base + h*head_stride + s*tok_stride
+ * (elements).  n_cached = total_cached; query s sits at n_cached - seq_len + s. */
+int genllm_paged_decode(const void *q, int64_t q_head_stride, int64_t q_tok_stride, void *out,
+                        int64_t o_head_stride, int64_t o_tok_stride, const void *k_pool, const void *v_pool,
+                        const int32_t *k_ids, const int32_t *v_ids, int32_t n_pages, int32_t n_cached,
+                        int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                        int32_t causal, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The same attention loop for long query chunks (prefill): bf16 MFMA
+ * FlashAttention over page-gathered K/V tiles, causal with query s at
+ * n_cached - seq_len + s. */
+int genllm_paged_prefill(const void *q, int64_t q_head_stride, int64_t q_tok_stride, void *out,
+                         int64_t o_head_stride, int64_t o_tok_stride, const void *k_pool, const void *v_pool,
+                         const int32_t *k_ids, const int32_t *v_ids, int32_t n_pages, int32_t n_cached,
+                         int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                         int32_t causal, void *stream);
+
+/* ------------------------------------------------------------ utilities
+ * No counterpart in the reference: synthetic seeded inputs for tests and the
+ * benchmark (counter-based hash -> Box-Muller -> RNE bf16). */
+int genllm_fill_normal_bf16(void *dst, size_t n, uint64_t seed, uint64_t offset, void *stream);
+
+/* No counterpart in the reference: runs one v_mfma_f32_16x16x32_bf16 on
+ * a[16][32], b[32][16] (bf16, device) into c[16][16] (fp32, device) through
+ * the operand layouts the kernels assume; the tests compare it with a host
+ * matrix product. */
+int genllm_selftest_mfma(const void *a, const void *b, float *c, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

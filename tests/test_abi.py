@@ -1,0 +1,66 @@
+"""CPU-side checks of the C ABI: libgenllm_hip.so loads without a GPU, exports
+every function include/genllm_paged.h declares, and its host-only entry points
+(RoPE table, workspace sizing, error reporting) behave."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+
+from genllm_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "genllm_paged.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(genllm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_functions_all_exported_and_bound():
+    names = declared_functions()
+    assert len(names) >= 20
+    L = _lib.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+    dyn = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (genllm_\w+)", dyn))
+    assert set(names) <= exported
+
+
+def test_rope_cache_matches_oracle(orc):
+    for D, S, theta in [(128, 4100, 1e6), (64, 300, 1e4)]:
+        cos = np.empty((S, D), np.float32)
+        sin = np.empty((S, D), np.float32)
+        _lib.call("genllm_rope_cache", cos.ctypes.data, theta, D, S, 1)
+        _lib.call("genllm_rope_cache", sin.ctypes.data, theta, D, S, 0)
+        oc, os_ = orc.rope_cache(theta, D, S)
+        assert np.array_equal(cos, oc) and np.array_equal(sin, os_)
+
+
+def test_errors_are_reported():
+    L = _lib.lib()
+    rc = L.genllm_rope_cache(None, 1e6, 128, 4, 1)
+    assert rc == _lib.ERR_INVALID
+    assert b"rope_cache" in L.genllm_last_error()
+    try:
+        _lib.call("genllm_rope_cache", None, 1e6, 128, 4, 1)
+    except _lib.GenllmError as e:
+        assert e.code == _lib.ERR_INVALID
+    else:
+        raise AssertionError("no error raised")
+
+
+def test_decode_workspace_closed_form():
+    L = _lib.lib()
+    # counters (Hkv * chunks ints, padded to 256 B) + partials (Hkv*chunks*pages*4 rows*(D+2) fp32)
+    for Hq, Hkv, S, D, pages in [(32, 8, 1, 128, 513), (16, 8, 1, 128, 64), (32, 8, 3, 128, 10)]:
+        chunks = (Hq // Hkv * S + 3) // 4
+        units = Hkv * chunks
+        want = ((units * 4 + 255) // 256) * 256 + units * pages * 4 * (D + 2) * 4
+        assert L.genllm_paged_decode_workspace_bytes(Hq, Hkv, S, D, pages) == want
+    assert L.genllm_paged_decode_workspace_bytes(0, 8, 1, 128, 4) == 0

@@ -1,0 +1,136 @@
+"""GPU parity of the split-K paged decode kernel (genllm_paged_decode) against
+the oracle's PagedAttentionImpl<CPU> attention loop, on identical pools and
+block tables.  Tolerance (bf16 output, fp32 accumulate): max-abs <= 2^-7 *
+max|ref| and rel-L2 <= 1e-2 (helpers.assert_attn_close)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from genllm_amd import paged, synth
+from helpers import assert_attn_close, oracle_fragmented, scale_for
+
+pytestmark = pytest.mark.gpu
+
+
+class Context:
+    """A GPU manager and an oracle manager holding the same n_ctx cached tokens
+    in identically fragmented pools (pool contents random everywhere, so
+    unfilled slots of the last page hold junk the kernels must ignore)."""
+
+    def __init__(self, orc, Hkv, D, pool, n_ctx, seed, nan_tail=False):
+        self.Hkv, self.D, self.pool = Hkv, D, pool
+        perm_k, perm_v = synth.shuffled(seed, pool), synth.shuffled(seed + 1, pool)
+        self.mgr = paged.PagedAttentionManager(2 * pool * 16 * Hkv * D * 2 + (1 << 20))
+        self.mgr.init_layer(0, Hkv, D)
+        self.mgr.reserve_layer(0, pool)
+        self.mgr.fragment(0, perm_k, perm_v)
+        self.mgr.append_kv_pages(0, n_ctx)
+        self.ref = oracle_fragmented(orc, Hkv, D, pool, perm_k, perm_v)
+        self.ref.append_kv_pages(0, n_ctx)
+        kp = synth.normal_bf16(seed + 2, (pool, 16, Hkv, D))
+        vp = synth.normal_bf16(seed + 3, (pool, 16, Hkv, D))
+        self.ref.pool_array(0, 0)[:] = kp
+        self.ref.pool_array(0, 1)[:] = vp
+        if nan_tail and n_ctx % 16:
+            kt, vt = self.ref.page_table(0)
+            kp = kp.copy()
+            vp = vp.copy()
+            kp[kt[-1], n_ctx % 16:] = 0x7FC0  # NaN in the unfilled slots (GPU copy only)
+            vp[vt[-1], n_ctx % 16:] = 0xFF80  # -inf
+        self.mgr.write_pool(0, 0, kp)
+        self.mgr.write_pool(0, 1, vp)
+        kt, vt = self.mgr.page_table(0)
+        rk, rv = self.ref.page_table(0)
+        assert np.array_equal(kt, rk) and np.array_equal(vt, rv)
+        self.info = self.mgr.get_layer(0)
+        self.n_ctx = n_ctx
+
+    def decode(self, q_bits, causal=True, pps=None):
+        Hq, S, D = q_bits.shape
+        out = torch.zeros((Hq, S, D), dtype=torch.bfloat16, device="cuda")
+        n_pages = (self.n_ctx + 15) // 16
+        ws = torch.zeros(paged.decode_workspace_bytes(Hq, self.Hkv, S, D, n_pages), dtype=torch.uint8,
+                         device="cuda")
+        old = os.environ.get("GENLLM_DECODE_PPS")
+        if pps:
+            os.environ["GENLLM_DECODE_PPS"] = str(pps)
+        try:
+            info = self.info
+            paged.paged_decode(paged.to_device_bf16(q_bits), out, info.k_pool, info.v_pool, info.k_ids, info.v_ids,
+                               n_pages, self.n_ctx, self.Hkv, scale_for(D), ws, causal=causal)
+            torch.cuda.synchronize()
+        finally:
+            if pps:
+                if old is None:
+                    del os.environ["GENLLM_DECODE_PPS"]
+                else:
+                    os.environ["GENLLM_DECODE_PPS"] = old
+        return paged.to_host_bits(out), ws
+
+    def oracle(self, q_bits, causal=True):
+        Hq, S, D = q_bits.shape
+        out, rc = self.ref.paged_attend(0, q_bits[None], self.Hkv, Hq // self.Hkv, scale_for(D), causal)
+        assert rc == 0
+        return out[0]
+
+    def close(self):
+        self.mgr.close()
+
+
+def test_decode_config1(orc):
+    """Qwen3-0.6B shape, 1024 cached tokens = 64 pages of a
+    randomly permuted 256-page pool, GQA 2:1."""
+    seed = synth.config_seed(1)
+    ctx = Context(orc, 8, 128, 256, 1024, seed)
+    q = synth.normal_bf16(seed, (16, 1, 128), offset=7 << 28)
+    got, _ = ctx.decode(q)
+    assert_attn_close(got, ctx.oracle(q), "config1")
+    ctx.close()
+
+
+@pytest.mark.parametrize("Hq,Hkv,N", [(32, 8, 1), (32, 8, 15), (32, 8, 16), (32, 8, 17), (16, 8, 100),
+                                      (8, 8, 33), (64, 8, 47), (32, 4, 250), (32, 8, 2049)])
+def test_decode_shapes(orc, Hq, Hkv, N):
+    pool = max(8, (N + 15) // 16 + 3)
+    ctx = Context(orc, Hkv, 128, pool, N, 1000 + N + Hq, nan_tail=True)
+    q = synth.normal_bf16(2000 + N, (Hq, 1, 128))
+    got, ws = ctx.decode(q)
+    assert_attn_close(got, ctx.oracle(q), f"Hq{Hq} Hkv{Hkv} N{N}")
+    # the split counters are back at zero after the launch
+    G = Hq // Hkv
+    units = Hkv * ((G + 3) // 4)
+    assert not ws[: units * 4].any().item()
+    ctx.close()
+
+
+@pytest.mark.parametrize("pps", [1, 2, 4, 8, 1000])
+def test_decode_split_plans(orc, pps):
+    ctx = Context(orc, 8, 128, 80, 1000, 77)
+    q = synth.normal_bf16(78, (32, 1, 128))
+    got, _ = ctx.decode(q, pps=pps)
+    assert_attn_close(got, ctx.oracle(q), f"pps{pps}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("S,Hq,causal", [(2, 32, True), (4, 32, True), (3, 16, True), (8, 16, True),
+                                         (2, 32, False)])
+def test_decode_multi_query(orc, S, Hq, causal):
+    """Short chunks (append_tokens with a few tokens): rows = (query, q head),
+    query s at n_cached - S + s; causal masks keys after it."""
+    N = 61
+    ctx = Context(orc, 8, 128, 8, N, 300 + S, nan_tail=True)
+    q = synth.normal_bf16(301 + S, (Hq, S, 128))
+    got, _ = ctx.decode(q, causal=causal)
+    assert_attn_close(got, ctx.oracle(q, causal), f"S{S} Hq{Hq} causal{causal}")
+    ctx.close()
+
+
+def test_decode_repeat_is_deterministic(orc):
+    ctx = Context(orc, 8, 128, 64, 900, 5)
+    q = synth.normal_bf16(6, (32, 1, 128))
+    a, _ = ctx.decode(q)
+    b, _ = ctx.decode(q)
+    assert np.array_equal(a, b)
+    ctx.close()

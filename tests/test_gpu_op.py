@@ -1,0 +1,149 @@
+"""The op end to end: genllm_paged_attention (PagedAttentionImpl<HIP>::execute)
+against the oracle's PagedAttentionImpl<CPU>::execute over a prefill /
+decode / append_tokens sequence, with the reference's state semantics (LIFO
+block pools, separate K/V ids, append-then-attend, reset), and its error paths."""
+import numpy as np
+import pytest
+import torch
+
+from genllm_amd import paged, synth
+from genllm_amd._lib import ERR_INVALID, ERR_POOL_FULL, ERR_UNSUPPORTED, GenllmError
+from helpers import assert_attn_close, oracle_fragmented, scale_for
+
+pytestmark = pytest.mark.gpu
+
+
+def make(orc, Hkv, D, pool, seed, layer=0):
+    perm_k, perm_v = synth.shuffled(seed, pool), synth.shuffled(seed + 1, pool)
+    mgr = paged.PagedAttentionManager(2 * pool * 16 * Hkv * D * 2 + (1 << 20))
+    mgr.init_layer(layer, Hkv, D)
+    mgr.reserve_layer(layer, pool)
+    mgr.fragment(layer, perm_k, perm_v)
+    ref = oracle_fragmented(orc, Hkv, D, pool, perm_k, perm_v, layer)
+    return mgr, ref
+
+
+def step(mgr, ref, layer, Hq, Hkv, S, D, seed, label):
+    G = Hq // Hkv
+    q = synth.normal_bf16(seed, (1, Hq, S, D))
+    k = synth.normal_bf16(seed + 1, (1, Hkv, S, D))
+    v = synth.normal_bf16(seed + 2, (1, Hkv, S, D))
+    out = torch.zeros((1, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    print(f"op step {label}: S={S}", flush=True)
+    paged.paged_attention(mgr, layer, paged.to_device_bf16(q), paged.to_device_bf16(k), paged.to_device_bf16(v), out,
+                          G, scale_for(D))
+    torch.cuda.synchronize()
+    want, rc = ref.paged_attention(layer, q, k, v, G, scale_for(D))
+    assert rc == 0
+    assert_attn_close(paged.to_host_bits(out), want, label)
+    kt, vt = mgr.page_table(layer)
+    rk, rv = ref.page_table(layer)
+    assert np.array_equal(kt, rk) and np.array_equal(vt, rv)
+    assert mgr.get_layer(layer).num_cached == ref.num_cached(layer)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (16, 8)])
+def test_op_prefill_decode_append_sequence(orc, Hq, Hkv):
+    D, pool = 128, 24
+    mgr, ref = make(orc, Hkv, D, pool, 11 + Hq)
+    seed = 500
+    step(mgr, ref, 0, Hq, Hkv, 40, D, seed, "prefill 40")              # MFMA prefill path
+    for i in range(20):                                                # decode, crossing pages 3 and 4
+        step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 10 * (i + 1), f"decode {41 + i}")
+    step(mgr, ref, 0, Hq, Hkv, 16 // (Hq // Hkv), D, seed + 999, "append_tokens")  # short chunk: decode kernel
+    step(mgr, ref, 0, Hq, Hkv, 100, D, seed + 1999, "append 100")      # chunked prefill on a warm cache
+    # the op appends K/V unmodified: both pools equal the oracle's bit for bit
+    assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0))
+    assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1))
+    # reset: host state rewinds like the reference; the next step reuses pages LIFO
+    mgr.reset()
+    ref.reset()
+    step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 7, "after reset")
+    mgr.close()
+
+
+def test_op_config3_decode_with_append(orc):
+    """Qwen3-4B decode at 8K context -- 512 full pages from a
+    shuffled 2048-page pool, append one token at 8192 (opens page 513), attend
+    over 8193 keys."""
+    seed = synth.config_seed(3)
+    Hq, Hkv, D, pool, N = 32, 8, 128, 2048, 8192
+    mgr, ref = make(orc, Hkv, D, pool, seed)
+    mgr.append_kv_pages(0, N)
+    ref.append_kv_pages(0, N)
+    kp = synth.normal_bf16(seed + 2, (pool, 16, Hkv, D))
+    vp = synth.normal_bf16(seed + 3, (pool, 16, Hkv, D))
+    ref.pool_array(0, 0)[:] = kp
+    ref.pool_array(0, 1)[:] = vp
+    mgr.write_pool(0, 0, kp)
+    mgr.write_pool(0, 1, vp)
+    step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 4, "config3")
+    assert mgr.get_layer(0).num_pages == 513
+    mgr.close()
+
+
+def test_op_errors_and_noops(orc):
+    D, Hkv = 128, 8
+    mgr, ref = make(orc, Hkv, D, 2, 3)
+    q = paged.to_device_bf16(synth.normal_bf16(1, (1, 16, 1, D)))
+    kv = paged.to_device_bf16(synth.normal_bf16(2, (1, Hkv, 1, D)))
+    out = torch.zeros((1, 16, 1, D), dtype=torch.bfloat16, device="cuda")
+    # inactive layer: silent no-op, output untouched (attention.cpp:127)
+    paged.paged_attention(mgr, 7, q, kv, kv, out, 2, 0.1)
+    torch.cuda.synchronize()
+    assert not out.float().abs().sum().item()
+    # head_dim != 128 is unsupported (attention.cu:511)
+    q64 = torch.zeros((1, 16, 1, 64), dtype=torch.bfloat16, device="cuda")
+    kv64 = torch.zeros((1, Hkv, 1, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(GenllmError) as e:
+        paged.paged_attention(mgr, 0, q64, kv64, kv64, q64.clone(), 2, 0.1)
+    assert e.value.code == ERR_UNSUPPORTED
+    # groups inconsistent with the head counts
+    with pytest.raises(GenllmError) as e:
+        paged.paged_attention(mgr, 0, q, kv, kv, out, 3, 0.1)
+    assert e.value.code == ERR_INVALID
+    # pool exhaustion: 2 pages hold 32 tokens; the 33rd is refused, state unchanged
+    big_q = paged.to_device_bf16(synth.normal_bf16(3, (1, 16, 32, D)))
+    big_kv = paged.to_device_bf16(synth.normal_bf16(4, (1, Hkv, 32, D)))
+    big_out = torch.zeros_like(big_q)
+    paged.paged_attention(mgr, 0, big_q, big_kv, big_kv, big_out, 2, 0.1)
+    before = (mgr.get_layer(0).num_cached, mgr.page_table(0))
+    with pytest.raises(GenllmError) as e:
+        paged.paged_attention(mgr, 0, q, kv, kv, out, 2, 0.1)
+    assert e.value.code == ERR_POOL_FULL
+    after = (mgr.get_layer(0).num_cached, mgr.page_table(0))
+    assert before[0] == after[0] == 32 and np.array_equal(before[1][0], after[1][0])
+    # set_page_table refuses ids the pool never handed out
+    with pytest.raises(GenllmError):
+        mgr.set_page_table(0, [5], [0], 16)
+    torch.cuda.synchronize()
+    mgr.close()
+
+
+def test_manager_state_machine_matches_oracle(orc):
+    """Host state only (no kernels): the reference's unit-test sequences on the
+    product's manager."""
+    mgr = paged.PagedAttentionManager(1 << 20)
+    mgr.init_layer(0, 8, 128)
+    assert mgr.is_active(0) and not mgr.is_active(2)
+    mgr.append_kv_pages(0, 1)   # no reserved pools: page logic only, like the pool-less fake
+    assert mgr.get_layer(0).num_cached == 1
+    mgr.append_kv_pages(0, 31)
+    assert mgr.get_layer(0).num_cached == 32 and mgr.get_layer(0).num_pages == 2
+    mgr.init_layer(1, 4, 64, 0)
+    mgr.append_kv_pages(1, 20)
+    mgr.reset()
+    assert mgr.get_layer(0).num_cached == 0 and mgr.get_layer(1).num_pages == 0
+    # block pools: ids 0,1, reuse of a freed id, LIFO after reset
+    mgr.init_layer(3, 8, 128)
+    mgr.reserve_layer(3, 10)
+    assert [mgr.block_alloc(3, 0) for _ in range(3)] == [0, 1, 2]
+    mgr.block_free(3, 0, 1)
+    assert mgr.block_alloc(3, 0) == 1
+    mgr.reset()
+    assert mgr.block_alloc(3, 0) == 2
+    for _ in range(9):
+        mgr.block_alloc(3, 1)
+    mgr.block_alloc(3, 1)
+    assert mgr.block_alloc(3, 1) == -1
+    mgr.close()

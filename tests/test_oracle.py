@@ -1,0 +1,434 @@
+"""Pins the CPU oracle (oracle/) before anything is compared with it.
+
+Every oracle function is checked against the reference's own unit-test values
+(tests/golden/reference_unit_cases.json) and against what mathematics fixes:
+closed forms in float64, brute-force attention, identities (RoPE at position 0,
+a single key, equal keys, one dominant key) and invariants (rotation
+composition and norm preservation, page placement in closed form).
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from genllm_amd import synth
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_unit_cases.json")))
+
+
+def f32(b):
+    return synth.bf16_bits_to_f32(b)
+
+
+def bf16_ulp(x):
+    """Spacing of bf16 at |x| (8 significant bits)."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(x, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+# ----------------------------------------------------------------- bf16
+def nearest_bf16_bruteforce(u):
+    """Nearest bf16 to each finite normal float (ties to even), from the two
+    neighbouring candidates in float64 -- a definition independent of the
+    carry-add formula."""
+    lo = (u >> np.uint32(16)).astype(np.uint32)
+    x = u.view(np.float32).astype(np.float64)
+    v_lo = ((lo << np.uint32(16)).view(np.float32)).astype(np.float64)
+    hi = lo + np.uint32(1)
+    v_hi = ((hi << np.uint32(16)).view(np.float32)).astype(np.float64)
+    d_lo = np.abs(x - v_lo)
+    d_hi = np.abs(v_hi - x)
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & ((lo & np.uint32(1)) == 1))
+    return np.where(pick_hi, hi, lo).astype(np.uint16)
+
+
+def test_bf16_roundtrip_reference_values(orc):
+    c = GOLDEN["bf16_roundtrip"]
+    vals = np.array(c["values"], dtype=np.float32)
+    back = f32(orc.f32_to_bf16(vals))
+    assert np.all(np.abs(back - vals) <= np.abs(vals) * 1e-2 + 1e-6)
+
+
+def test_bf16_special_values(orc):
+    L = orc.lib()
+    assert L.or_f32_to_bf16(float("inf")) == GOLDEN["bf16_special"]["infinity_bits"]
+    assert L.or_f32_to_bf16(float("-inf")) == GOLDEN["bf16_special"]["neg_infinity_bits"]
+    assert L.or_f32_to_bf16(float("nan")) == 0x7F81  # mantissa != 0 -> low bit set
+    assert L.or_f32_to_bf16(0.0) == GOLDEN["bf16_special"]["zero_bits"]
+    assert L.or_f32_to_bf16(-0.0) == 0x8000
+    assert L.or_f32_to_bf16(1e-40) == 0x0000  # subnormal flushes to signed zero
+    assert L.or_f32_to_bf16(-1e-40) == 0x8000
+    assert L.or_f32_to_bf16(3.3895313892515355e38) == 0x7F7F  # max bf16 stays finite
+    assert L.or_f32_to_bf16(np.float32(3.4028235e38)) == 0x7F80  # rounds up to inf
+    # NaN payloads all collapse to 0x7F81/0xFF81
+    nan_bits = np.array([0x7FC00000, 0x7F800001, 0xFFC12345], dtype=np.uint32)
+    got = orc.f32_to_bf16(nan_bits.view(np.float32))
+    assert list(got) == [0x7F81, 0x7F81, 0xFF81]
+
+
+def test_bf16_rne_matches_nearest(orc):
+    rng = np.random.default_rng(7)
+    u = rng.integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    e = (u >> 23) & 0xFF
+    u = u[(e != 0) & (e != 0xFF) & ~((e == 0xFE) & (((u >> 16) & 0x7F) == 0x7F))]  # finite, no overflow
+    ties = (rng.integers(0, 2 ** 16, size=4096).astype(np.uint32) << 16) | np.uint32(0x8000)
+    te = (ties >> 23) & 0xFF
+    ties = ties[(te != 0) & (te < 0xFE)]
+    u = np.concatenate([u, ties])
+    got = orc.f32_to_bf16(u.view(np.float32))
+    assert np.array_equal(got, nearest_bf16_bruteforce(u))
+    # the product's host conversion agrees with the oracle bit for bit
+    assert np.array_equal(synth.f32_to_bf16_bits(u.view(np.float32)), got)
+
+
+# ------------------------------------------------------------ block pool
+def test_block_pool_reference_sequences(orc):
+    c = GOLDEN["block_pool_alloc_free"]
+    p = orc.BlockPool(c["capacity"])
+    for op, val in c["steps"]:
+        if op == "alloc":
+            assert p.alloc() == val
+        elif op == "free":
+            p.free(val)
+        elif op == "num_blocks":
+            assert p.num_blocks() == val
+        elif op == "num_free":
+            assert p.num_free() == val
+    c = GOLDEN["block_pool_many_allocs"]
+    p = orc.BlockPool(c["capacity"])
+    assert all(p.alloc() >= 0 for _ in range(c["allocs_ok"]))
+    assert p.alloc() == c["then"]
+    c = GOLDEN["block_pool_reset"]
+    p = orc.BlockPool(c["capacity"])
+    for _ in range(c["allocs"]):
+        p.alloc()
+    p.reset()
+    assert p.num_blocks() == c["after_reset"]["num_blocks"]
+    assert p.num_free() == c["after_reset"]["num_free"]
+    assert p.alloc() == c["next_alloc"]
+
+
+def test_block_pool_lifo_and_free_bounds(orc):
+    p = orc.BlockPool(8)
+    ids = [p.alloc() for _ in range(5)]
+    assert ids == [0, 1, 2, 3, 4]
+    p.free(7)  # never handed out: ignored
+    p.free(-1)
+    assert p.num_free() == 0
+    p.free(3)
+    p.free(1)
+    assert p.alloc() == 1 and p.alloc() == 3 and p.alloc() == 5
+
+
+def test_manager_reference_sequences(orc):
+    c = GOLDEN["page_table_append_kv"]
+    m = orc.Manager(with_pool=False)
+    m.init_layer(0, 8, 128)
+    assert m.is_active(0) and m.num_cached(0) == 0
+    m.append_kv_pages(0, 1)
+    assert m.num_cached(0) == 1
+    m.append_kv_pages(0, 31)
+    assert m.num_cached(0) == 32 and m.num_pages(0) == 2
+    c = GOLDEN["page_table_multi_layer"]
+    m = orc.Manager(with_pool=False)
+    m.init_layer(0, 8, 128, 1)
+    m.init_layer(1, 4, 64, 0)
+    assert m.is_active(0) and m.is_active(1) and not m.is_active(c["inactive_layer"])
+    m.append_kv_pages(0, 5)
+    m.append_kv_pages(1, 20)
+    assert m.num_cached(0) == 5 and m.num_cached(1) == 20
+    m.reset()
+    assert m.num_cached(0) == 0 and m.num_pages(1) == 0
+
+
+def test_manager_page_opening_closed_form(orc):
+    """A page opens exactly at positions g with g % 16 == 0; ids are handed out
+    in allocation order; after reset the free list returns n-1 first."""
+    m = orc.Manager(with_pool=True)
+    m.init_layer(3, 2, 8)
+    m.reserve_layer(3, 10)
+    total = 0
+    for c in [1, 15, 1, 16, 17, 3]:
+        m.append_kv_pages(3, c)
+        total += c
+        assert m.num_cached(3) == total
+        assert m.num_pages(3) == (total + 15) // 16
+    k, v = m.page_table(3)
+    assert list(k) == list(range(len(k))) and list(v) == list(range(len(v)))
+    m.reset()
+    m.append_kv_pages(3, 33)
+    k, _ = m.page_table(3)
+    assert list(k) == [3, 2, 1]  # 4 pages were handed out; reset's free list pops the highest id first
+
+
+def test_manager_exhaustion_reference_behaviour(orc):
+    """The reference breaks out of the loop on a failed allocation but still
+    advances num_cached (page_attention.cpp:155,161)."""
+    m = orc.Manager(with_pool=True)
+    m.init_layer(0, 1, 8)
+    m.reserve_layer(0, 2)
+    m.append_kv_pages(0, 40)
+    assert m.num_cached(0) == 40 and m.num_pages(0) == 2
+
+
+# --------------------------------------------------------------- rms norm
+def test_rms_norm_reference_values(orc):
+    c = GOLDEN["rms_norm"]
+    x = synth.f32_to_bf16_bits(np.array(c["x"], dtype=np.float32))
+    out = f32(orc.rms_norm(x, np.array(c["gamma"], dtype=np.float32), c["eps"])).ravel()
+    for chk in c["checks"]:
+        assert abs(out[chk["index"]] - chk["expected"]) <= c["tolerance"]
+
+
+@pytest.mark.parametrize("hidden", [128, 64, 256, 12, 4, 40])
+def test_rms_norm_closed_form(orc, hidden):
+    rows = 257
+    x = synth.normal_bf16(11, (rows, hidden))
+    w = synth.uniform_f32(12, (hidden,), 0.5, 1.5)
+    eps = 1e-6
+    got = f32(orc.rms_norm(x, w, eps)).astype(np.float64)
+    xd = f32(x).astype(np.float64)
+    y = xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + eps) * w.astype(np.float64)
+    vec_end = (hidden // 8) * 8
+    # whole 8-blocks are truncated toward zero: |got| <= |y| (up to fp32 error), within one bf16 ulp
+    err = np.abs(got - y)
+    assert np.all(err[:, :vec_end] <= bf16_ulp(y[:, :vec_end]) * 1.01 + 1e-30)
+    assert np.all(np.abs(got[:, :vec_end]) <= np.abs(y[:, :vec_end]) * (1 + 2e-6) + 1e-30)
+    # the scalar tail is rounded to nearest: within half an ulp
+    if vec_end < hidden:
+        assert np.all(err[:, vec_end:] <= bf16_ulp(y[:, vec_end:]) * 0.51 + 1e-30)
+
+
+# ------------------------------------------------------------------- rope
+def test_rope_cache_closed_form(orc):
+    D, S, theta = 128, 4099, 1e6
+    cos, sin = orc.rope_cache(theta, D, S)
+    half = D // 2
+    assert np.array_equal(cos[:, :half], cos[:, half:]) and np.array_equal(sin[:, :half], sin[:, half:])
+    inv = np.array([1.0 / math.pow(theta, 2.0 * i / D) for i in range(half)])
+    rows = list(range(0, S, 97)) + [S - 1]
+    for s in rows:
+        ec = np.array([math.cos(s * f) for f in inv], dtype=np.float32)
+        es = np.array([math.sin(s * f) for f in inv], dtype=np.float32)
+        assert np.array_equal(cos[s, :half], ec) and np.array_equal(sin[s, :half], es)
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+
+
+def test_apply_rope_position_zero_is_identity(orc):
+    cos, sin = orc.rope_cache(1e6, 128, 8)
+    x = synth.normal_bf16(21, (3, 5, 128))
+    x[x == 0] = 0x3F80
+    x[x == 0x8000] = 0x3F80
+    out = orc.apply_rope(x[:, :1], cos, sin, 0)
+    assert np.array_equal(out, x[:, :1])
+
+
+def test_apply_rope_closed_form_and_invariants(orc):
+    D = 128
+    cos, sin = orc.rope_cache(1e6, D, 64)
+    x = synth.normal_bf16(22, (4, 16, D))
+    start = 9
+    got = f32(orc.apply_rope(x, cos, sin, start)).astype(np.float64)
+    xd = f32(x).astype(np.float64)
+    half = D // 2
+    pos = start + np.arange(16)[None, :, None]
+    ang = pos * np.array([1e6 ** (-2.0 * i / D) for i in range(half)])[None, None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    x0, x1 = xd[..., :half], xd[..., half:]
+    want = np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
+    assert np.all(np.abs(got - want) <= bf16_ulp(want) * 0.6 + 1e-6)
+    # rotation keeps each pair's norm
+    n_in = x0 ** 2 + x1 ** 2
+    n_out = got[..., :half] ** 2 + got[..., half:] ** 2
+    assert np.allclose(n_in, n_out, rtol=2e-2, atol=1e-3)
+    # composing rotations: rope(rope(x, a), b) == rope(x, a + b) up to two bf16 roundings
+    a, b = 5, 7
+    once = f32(orc.apply_rope(x, cos, sin, a + b)).astype(np.float64)
+    cos_b = np.ascontiguousarray(np.tile(cos[b], (16, 1)))  # every row rotated by angle(b)
+    sin_b = np.ascontiguousarray(np.tile(sin[b], (16, 1)))
+    twice = f32(orc.apply_rope(orc.apply_rope(x, cos, sin, a), cos_b, sin_b, 0)).astype(np.float64)
+    assert np.max(np.abs(once - twice)) <= 4 * np.max(bf16_ulp(once))
+
+
+# ----------------------------------------------------------------- append
+def fragmented(orc, Hkv, D, pool, perm_k, perm_v, layer=0):
+    m = orc.Manager(with_pool=True)
+    m.init_layer(layer, Hkv, D)
+    m.reserve_layer(layer, pool)
+    for which, perm in ((0, perm_k), (1, perm_v)):
+        p = m.pool(layer, which)
+        for _ in range(pool):
+            p.alloc()
+        for b in perm[::-1]:
+            p.free(int(b))
+    return m
+
+
+def test_append_page_placement_closed_form(orc):
+    Hkv, D, pool = 3, 16, 12
+    perm_k, perm_v = synth.shuffled(1, pool), synth.shuffled(2, pool)
+    m = fragmented(orc, Hkv, D, pool, perm_k, perm_v)
+    pos = 0
+    chunks = []
+    for S in [5, 11, 1, 16, 20]:
+        K = synth.normal_bf16(100 + S, (Hkv, S, D))
+        V = synth.normal_bf16(200 + S, (Hkv, S, D))
+        m.append_kv_from_tensor(0, K, V)
+        chunks.append((pos, K, V))
+        pos += S
+    k_ids, v_ids = m.page_table(0)
+    n_pages = (pos + 15) // 16
+    assert list(k_ids) == list(perm_k[:n_pages]) and list(v_ids) == list(perm_v[:n_pages])
+    kp, vp = m.pool_array(0, 0), m.pool_array(0, 1)
+    for p0, K, V in chunks:
+        for t in range(K.shape[1]):
+            g = p0 + t
+            assert np.array_equal(kp[k_ids[g // 16], g % 16], K[:, t, :])
+            assert np.array_equal(vp[v_ids[g // 16], g % 16], V[:, t, :])
+    # slots past the last token stay zero (pools start zeroed)
+    last = pos % 16
+    assert not kp[k_ids[-1], last:].any() and not vp[v_ids[-1], last:].any()
+
+
+# -------------------------------------------------------------- attention
+def brute_attention(q, K, V, groups, scale, causal, n_cached):
+    """float64 softmax(q K^T scale) V; q [Hq][S][D], K/V [Hkv][N][D] (float)."""
+    Hq, S, D = q.shape
+    out = np.zeros((Hq, S, D))
+    for h in range(Hq):
+        kv = h // groups
+        for s in range(S):
+            q_abs = n_cached - S + s
+            lim = q_abs + 1 if causal else n_cached
+            sc = K[kv, :lim] @ q[h, s] * scale
+            w = np.exp(sc - sc.max())
+            out[h, s] = (w / w.sum()) @ V[kv, :lim]
+    return out
+
+
+def run_paged(orc, Hq, Hkv, D, chunks, pool=16, causal=True, seed=0):
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D)
+    m = fragmented(orc, Hkv, D, pool, synth.shuffled(seed + 1, pool), synth.shuffled(seed + 2, pool))
+    Ks, Vs, outs, qs = [], [], [], []
+    for i, S in enumerate(chunks):
+        q = synth.normal_bf16(seed + 10 + i, (1, Hq, S, D))
+        K = synth.normal_bf16(seed + 30 + i, (1, Hkv, S, D))
+        V = synth.normal_bf16(seed + 50 + i, (1, Hkv, S, D))
+        out, rc = m.paged_attention(0, q, K, V, G, scale, causal)
+        assert rc == 0
+        Ks.append(K[0]), Vs.append(V[0]), qs.append(q[0]), outs.append(out[0])
+    return m, qs, Ks, Vs, outs, scale
+
+
+@pytest.mark.parametrize("chunks", [[1], [7], [5, 1, 1], [20, 3], [16, 16, 1]])
+def test_paged_attention_bruteforce(orc, chunks):
+    Hq, Hkv, D = 4, 2, 32
+    m, qs, Ks, Vs, outs, scale = run_paged(orc, Hq, Hkv, D, chunks)
+    n = 0
+    for q, o, S in zip(qs, outs, chunks):
+        n += S
+        K = f32(np.concatenate(Ks, axis=1)[:, :n]).astype(np.float64)
+        V = f32(np.concatenate(Vs, axis=1)[:, :n]).astype(np.float64)
+        want = brute_attention(f32(q).astype(np.float64), K, V, Hq // Hkv, scale, True, n)
+        got = f32(o).astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 2.0 ** -8 * np.max(np.abs(want)) + 1e-6
+
+
+def test_paged_attention_non_causal(orc):
+    Hq, Hkv, D = 2, 1, 16
+    chunks = [9, 6]
+    m, qs, Ks, Vs, outs, scale = run_paged(orc, Hq, Hkv, D, chunks, causal=False)
+    K = f32(np.concatenate(Ks, axis=1)).astype(np.float64)
+    V = f32(np.concatenate(Vs, axis=1)).astype(np.float64)
+    want = brute_attention(f32(qs[1]).astype(np.float64), K, V, 2, scale, False, 15)
+    assert np.max(np.abs(f32(outs[1]) - want)) <= 2.0 ** -8 * np.max(np.abs(want)) + 1e-6
+
+
+def test_paged_attention_single_key_is_exact(orc):
+    """One cached key: softmax weight 1, so out == bf16(v) bit for bit."""
+    m, qs, Ks, Vs, outs, _ = run_paged(orc, 4, 2, 32, [1])
+    assert np.array_equal(outs[0][0::2, 0], Vs[0][:, 0]) and np.array_equal(outs[0][1::2, 0], Vs[0][:, 0])
+
+
+def test_paged_attention_equal_keys_give_mean(orc):
+    Hq, Hkv, D, N = 2, 1, 16, 23
+    m = fragmented(orc, Hkv, D, 8, np.arange(8), np.arange(8))
+    K = np.tile(synth.normal_bf16(5, (1, 1, 1, D)), (1, 1, N, 1))
+    V = synth.normal_bf16(6, (1, 1, N, D))
+    q = synth.normal_bf16(7, (1, Hq, N, D))
+    out, _ = m.paged_attention(0, q, K, V, 2, 0.25, causal=False)
+    mean = f32(V[0, 0]).astype(np.float64).mean(axis=0)
+    assert np.max(np.abs(f32(out[0, :, -1]) - mean)) <= 2.0 ** -7 * np.max(np.abs(mean)) + 1e-3
+
+
+def test_paged_attention_dominant_key_selects_its_value(orc):
+    Hq, Hkv, D, N = 1, 1, 16, 40
+    m = fragmented(orc, Hkv, D, 8, np.arange(8)[::-1].copy(), np.arange(8))
+    K = np.zeros((1, 1, N, D), dtype=np.uint16)
+    K[0, 0, 17] = synth.f32_to_bf16_bits(np.full(D, 4.0, dtype=np.float32))
+    V = synth.normal_bf16(8, (1, 1, N, D))
+    q = np.zeros((1, Hq, N, D), dtype=np.uint16)
+    q[0, 0, -1] = synth.f32_to_bf16_bits(np.full(D, 4.0, dtype=np.float32))
+    out, _ = m.paged_attention(0, q, K, V, 1, 1.0, causal=True)
+    assert np.array_equal(out[0, 0, -1], V[0, 0, 17])
+
+
+def test_paged_attention_gqa_head_map(orc):
+    """q head h reads kv head h // groups (attention.cpp:158): swapping two kv
+    heads' data swaps exactly the outputs of their q-head groups."""
+    Hq, Hkv, D = 6, 3, 16
+    m1, qs, Ks, Vs, outs, scale = run_paged(orc, Hq, Hkv, D, [9], seed=40)
+    m2 = fragmented(orc, Hkv, D, 16, synth.shuffled(41, 16), synth.shuffled(42, 16))
+    K = Ks[0][[1, 0, 2]][None]
+    V = Vs[0][[1, 0, 2]][None]
+    q = qs[0][[2, 3, 0, 1, 4, 5]][None]
+    out2, _ = m2.paged_attention(0, q, K, V, 2, scale)
+    assert np.array_equal(out2[0][[2, 3, 0, 1, 4, 5]], outs[0])
+
+
+def test_paged_attention_inactive_layer_untouched(orc):
+    m = orc.Manager(with_pool=True)
+    q = synth.normal_bf16(1, (1, 2, 1, 16))
+    out, rc = m.paged_attention(5, q, q[:, :1], q[:, :1], 2, 0.25)
+    assert rc == 1 and not out.any()
+
+
+def test_flash_attention_bruteforce(orc):
+    Hq, Hkv, S, D = 4, 2, 19, 32
+    q = synth.normal_bf16(60, (1, Hq, S, D))
+    K = synth.normal_bf16(61, (1, Hkv, S, D))
+    V = synth.normal_bf16(62, (1, Hkv, S, D))
+    for causal in (True, False):
+        got = f32(orc.flash_attention(q, K, V, 2, 0.2, causal)[0]).astype(np.float64)
+        want = brute_attention(f32(q[0]).astype(np.float64), f32(K[0]).astype(np.float64),
+                               f32(V[0]).astype(np.float64), 2, 0.2, causal, S)
+        assert np.max(np.abs(got - want)) <= 2.0 ** -8 * np.max(np.abs(want)) + 1e-6
+
+
+def test_qk_norm_rope_append_composition(orc):
+    """The fused composition equals permute -> rms_norm -> apply_rope ->
+    append done step by step with the primitives."""
+    S, Hq, Hkv, D, pool = 21, 4, 2, 64, 8
+    cos, sin = orc.rope_cache(1e6, D, 64)
+    k = synth.normal_bf16(70, (S, Hkv, D))
+    v = synth.normal_bf16(71, (S, Hkv, D))
+    q = synth.normal_bf16(72, (S, Hq, D))
+    gk = synth.uniform_f32(73, (D,), 0.5, 1.5)
+    gq = synth.uniform_f32(74, (D,), 0.5, 1.5)
+    m = fragmented(orc, Hkv, D, pool, synth.shuffled(75, pool), synth.shuffled(76, pool))
+    m.append_kv_pages(0, 5)  # start mid-page
+    q_out = m.qk_norm_rope_append(0, k, v, gk, 1e-6, cos, sin, 5, q_tok=q, gamma_q=gq)
+    kh = np.ascontiguousarray(k.transpose(1, 0, 2))
+    qh = np.ascontiguousarray(q.transpose(1, 0, 2))
+    k_rope = orc.apply_rope(orc.rms_norm(kh, gk, 1e-6), cos, sin, 5)
+    assert np.array_equal(q_out, orc.apply_rope(orc.rms_norm(qh, gq, 1e-6), cos, sin, 5))
+    k_ids, v_ids = m.page_table(0)
+    kp, vp = m.pool_array(0, 0), m.pool_array(0, 1)
+    for t in range(S):
+        g = 5 + t
+        assert np.array_equal(kp[k_ids[g // 16], g % 16], k_rope[:, t])
+        assert np.array_equal(vp[v_ids[g // 16], g % 16], v[t])
