@@ -1,0 +1,350 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged KV-cache attention path (one GPU).
+
+Headline workload: Qwen3-4B-shape decode, batch 1 --
+one step = the op genllm_paged_attention (PagedAttentionImpl::execute):
+append one token's K/V, then split-K attention over ~8193 cached keys
+(q [1,32,1,128], 8 KV heads, 512+ pages drawn from a shuffled 2048-page pool).
+Steps rotate over 16 independent layers (~540 MB of touched KV) so the 256 MB
+MALL cannot serve them; each layer's context grows by one token per visit, as
+in a real decode loop, and the algorithmic bytes are counted per step.
+
+value = whole-step algorithmic HBM bytes / step time (GB/s).  roofline = the
+dominant kernel (paged_decode_kernel) timed alone with HIP events around each
+launch on the launch stream, against 8 TB/s.  Secondary figures (same line):
+config 2 fused append GB/s, config 4 causal prefill TFLOPS, config 5 36-layer
+long-context decode.  cpu_baseline = the oracle (single thread) on a bounded
+sample of the headline workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = ("paged decode attn µs/layer + achieved HBM GB/s (Qwen3-4B, 8K ctx); prefill TFLOPS")
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+PAGE = 16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
+    ap.add_argument("--skip-secondary", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def decode_step_bytes(n_keys: int, Hq=32, Hkv=8, D=128) -> int:
+    """Algorithmic bytes of one op step: K/V reads of n_keys tokens, the appended
+    token's K/V read + write, q read, out write, page ids (k and v) read."""
+    kv = n_keys * Hkv * D * 2 * 2
+    append = 2 * (2 * Hkv * D * 2)
+    qo = 2 * Hq * D * 2
+    ids = ((n_keys + PAGE - 1) // PAGE) * 8
+    return kv + append + qo + ids
+
+
+def decode_kernel_bytes(n_keys: int, Hq=32, Hkv=8, D=128) -> int:
+    return n_keys * Hkv * D * 2 * 2 + 2 * Hq * D * 2 + ((n_keys + PAGE - 1) // PAGE) * 8
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
+              "multi-GPU sharding of the path is described in DESIGN.md, not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from genllm_amd import paged, synth
+    from genllm_amd._lib import call as _call
+
+    torch.cuda.set_device(0)
+    dev_name = torch.cuda.get_device_name(0)
+    Hq, Hkv, D = 32, 8, 128
+    G = Hq // Hkv
+    scale = 1.0 / np.sqrt(D)
+    pool_pages = 2048
+    n0 = 8192
+    L = args.layers
+    seed = synth.config_seed(3)
+    layer_bytes = 2 * pool_pages * PAGE * Hkv * D * 2 + 4 * pool_pages * 4 + 4096
+    mgr = paged.PagedAttentionManager(L * layer_bytes + (1 << 20))
+    for l in range(L):
+        mgr.init_layer(l, Hkv, D)
+        mgr.reserve_layer(l, pool_pages)
+        mgr.fragment(l, synth.shuffled(seed + 2 * l, pool_pages), synth.shuffled(seed + 2 * l + 1, pool_pages))
+        mgr.append_kv_pages(l, n0)
+        info = mgr.get_layer(l)
+        n_el = pool_pages * PAGE * Hkv * D
+        _call("genllm_fill_normal_bf16", info.k_pool, n_el, seed + 100 + l, 0, None)
+        _call("genllm_fill_normal_bf16", info.v_pool, n_el, seed + 200 + l, 0, None)
+    q = [paged.to_device_bf16(synth.normal_bf16(seed + 300 + l, (1, Hq, 1, D))) for l in range(L)]
+    kn = [paged.to_device_bf16(synth.normal_bf16(seed + 400 + l, (1, Hkv, 1, D))) for l in range(L)]
+    vn = [paged.to_device_bf16(synth.normal_bf16(seed + 500 + l, (1, Hkv, 1, D))) for l in range(L)]
+    out = [torch.empty((1, Hq, 1, D), dtype=torch.bfloat16, device="cuda") for _ in range(L)]
+    torch.cuda.synchronize()
+
+    cached = [n0] * L
+
+    def op_step(i):
+        l = i % L
+        paged.paged_attention(mgr, l, q[l], kn[l], vn[l], out[l], G, scale)
+        cached[l] += 1
+        return decode_step_bytes(cached[l])
+
+    for i in range(args.warmup):
+        op_step(i)
+    torch.cuda.synchronize()
+    total_bytes = 0
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        total_bytes += op_step(args.warmup + i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    step_s = (t1 - t0) / args.steps
+    value_gbs = total_bytes / (t1 - t0) / 1e9
+    mean_keys = total_bytes / args.steps  # for the record only
+
+    # ---- dominant kernel alone: split-K decode, 8193 keys, HIP events per launch
+    n_keys = n0 + 1
+    ws = torch.zeros(paged.decode_workspace_bytes(Hq, Hkv, 1, D, pool_pages), dtype=torch.uint8, device="cuda")
+    infos = [mgr.get_layer(l) for l in range(L)]
+    o2 = torch.empty((Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    qh = [t.view(Hq, 1, D) for t in q]
+
+    def kernel_launch(i):
+        l = i % L
+        inf = infos[l]
+        paged.paged_decode(qh[l], o2, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, (n_keys + 15) // 16, n_keys,
+                           Hkv, scale, ws)
+
+    for i in range(args.warmup):
+        kernel_launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        kernel_launch(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    k_ms = [a.elapsed_time(b) for a, b in ev]
+    k_avg_us = 1e3 * sum(k_ms) / len(k_ms)
+    kbytes = decode_kernel_bytes(n_keys)
+    achieved = kbytes / (k_avg_us * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded counter-based normal bf16 K/V/q, Fisher-Yates block tables)",
+        "config": {"workload": "BASELINE config 3: Qwen3-4B-shape paged decode, batch 1, 8K context, "
+                               "append 1 token then attend (op genllm_paged_attention)",
+                   "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context_start": n0 + 1,
+                   "context_end": max(cached), "pool_pages": pool_pages, "rotating_layers": L},
+        "us_per_layer": round(step_s * 1e6, 2),
+        "device": dev_name,
+        "roofline": {"kernel": "paged_decode_kernel<128>", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": kbytes, "avg_launch_us": round(k_avg_us, 3),
+                     "p10_us": round(1e3 * np.percentile(k_ms, 10), 3),
+                     "p90_us": round(1e3 * np.percentile(k_ms, 90), 3)},
+    }
+
+    if not args.skip_secondary:
+        result["secondary"] = secondary(paged, synth, np, torch, args)
+
+    if not args.skip_cpu:
+        result["cpu_baseline"] = cpu_baseline(mgr, paged, synth, np, args, seed)
+    mgr.close()
+    print(json.dumps(result), flush=True)
+
+
+def time_launches(torch, fn, n, warm=5):
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record(stream)
+        fn(warm + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return 1e3 * sum(ms) / len(ms), ms
+
+
+def secondary(paged, synth, np, torch, args):
+    out = {}
+    # ---- config 2: fused K/V append (q/k norm -> RoPE -> scatter), 4096 tokens
+    S, Hkv, D, pool = 4096, 8, 128, 1024
+    seed = synth.config_seed(2)
+    copies = 8
+    m2 = paged.PagedAttentionManager(copies * (2 * pool * PAGE * Hkv * D * 2 + 8 * pool + 4096) + (1 << 20))
+    ks, vs = [], []
+    for c in range(copies):
+        m2.init_layer(c, Hkv, D)
+        m2.reserve_layer(c, pool)
+        m2.fragment(c, synth.shuffled(seed + 2 * c, pool), synth.shuffled(seed + 2 * c + 1, pool))
+        k = torch.empty((S, Hkv, D), dtype=torch.bfloat16, device="cuda")
+        v = torch.empty_like(k)
+        paged.fill_normal_bf16(k, seed + 10 + c)
+        paged.fill_normal_bf16(v, seed + 20 + c)
+        ks.append(k)
+        vs.append(v)
+    gamma = torch.from_numpy(synth.uniform_f32(seed, (D,), 0.5, 1.5)).cuda()
+    cos, sin = paged.rope_cache(1e6, D, S)
+    cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    n_app = copies * (pool // (S // PAGE))  # each copy takes 4 chunks of 256 pages
+
+    def app(i):
+        c = i % copies
+        paged.qk_norm_rope_append(m2, c, ks[c], vs[c], gamma, 1e-6, cos_d, sin_d, 0)
+
+    avg_us, _ = time_launches(torch, app, n_app, warm=0)
+    app_bytes = 2 * S * Hkv * D * 2 * 2 + S * (D // 2) * 4 * 2 + D * 4 + (S // PAGE) * 8
+    out["append_config2"] = {"avg_launch_us": round(avg_us, 3), "bytes": app_bytes,
+                             "GB_s": round(app_bytes / (avg_us * 1e-6) / 1e9, 1),
+                             "frac_hbm": round(app_bytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             "launches": n_app}
+    m2.close()
+
+    # ---- config 4: causal paged prefill, 2048 tokens, Qwen3-1.7B shape
+    Hq, Hkv, D, S = 16, 8, 128, 2048
+    seed = synth.config_seed(4)
+    copies = 4
+    m4 = paged.PagedAttentionManager(copies * (2 * 128 * PAGE * Hkv * D * 2 + 8 * 128 + 4096) + (1 << 20))
+    qs = []
+    from genllm_amd._lib import call as _call
+    for c in range(copies):
+        m4.init_layer(c, Hkv, D)
+        m4.reserve_layer(c, 128)
+        m4.fragment(c, synth.shuffled(seed + 2 * c, 128), synth.shuffled(seed + 2 * c + 1, 128))
+        m4.append_kv_pages(c, S)
+        inf = m4.get_layer(c)
+        _call("genllm_fill_normal_bf16", inf.k_pool, 128 * PAGE * Hkv * D, seed + 30 + c, 0, None)
+        _call("genllm_fill_normal_bf16", inf.v_pool, 128 * PAGE * Hkv * D, seed + 40 + c, 0, None)
+        qq = torch.empty((S, Hq, D), dtype=torch.bfloat16, device="cuda")
+        paged.fill_normal_bf16(qq, seed + 50 + c)
+        qs.append(qq)
+    o4 = torch.empty((S, Hq, D), dtype=torch.bfloat16, device="cuda")
+    infos = [m4.get_layer(c) for c in range(copies)]
+
+    def pre(i):
+        c = i % copies
+        inf = infos[c]
+        paged.paged_prefill(qs[c], o4, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, 128, S, Hkv, 1.0 / np.sqrt(D),
+                            q_layout="token")
+
+    avg_us, _ = time_launches(torch, pre, 40)
+    flops = 4 * D * Hq * S * (S + 1) // 2
+    tfl = flops / (avg_us * 1e-6) / 1e12
+    out["prefill_config4"] = {"avg_launch_us": round(avg_us, 3), "flops": flops, "TFLOPS": round(tfl, 1),
+                              "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}
+    m4.close()
+
+    # ---- config 5: 36 layers back-to-back, 32761 cached tokens each
+    Hq, Hkv, D, N, pool, layers = 32, 8, 128, 32761, 4096, 36
+    seed = synth.config_seed(5)
+    m5 = paged.PagedAttentionManager(layers * (2 * pool * PAGE * Hkv * D * 2 + 8 * pool + 4096) + (1 << 20))
+    for l in range(layers):
+        m5.init_layer(l, Hkv, D)
+        m5.reserve_layer(l, pool)
+        m5.fragment(l, synth.shuffled(seed + 2 * l, pool), synth.shuffled(seed + 2 * l + 1, pool))
+        m5.append_kv_pages(l, N)
+        inf = m5.get_layer(l)
+        _call("genllm_fill_normal_bf16", inf.k_pool, pool * PAGE * Hkv * D, seed + 100 + l, 0, None)
+        _call("genllm_fill_normal_bf16", inf.v_pool, pool * PAGE * Hkv * D, seed + 200 + l, 0, None)
+    q5 = torch.empty((layers, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    paged.fill_normal_bf16(q5, seed)
+    o5 = torch.empty((Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(paged.decode_workspace_bytes(Hq, Hkv, 1, D, pool), dtype=torch.uint8, device="cuda")
+    infos = [m5.get_layer(l) for l in range(layers)]
+    n_pages = (N + 15) // 16
+
+    def all_layers(_):
+        for l in range(layers):
+            inf = infos[l]
+            paged.paged_decode(q5[l], o5, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, n_pages, N, Hkv,
+                               1.0 / np.sqrt(D), ws)
+
+    avg_us, _ = time_launches(torch, all_layers, 10, warm=2)
+    b5 = layers * decode_kernel_bytes(N)
+    out["longctx_config5"] = {"total_us": round(avg_us, 2), "us_per_layer": round(avg_us / layers, 3),
+                              "bytes": b5, "GB_s": round(b5 / (avg_us * 1e-6) / 1e9, 1),
+                              "frac_hbm": round(b5 / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    m5.close()
+    return out
+
+
+def cpu_baseline(mgr, paged, synth, np, args, seed):
+    """The oracle (oracle/, single thread) on the headline step, on inputs
+    copied back from layer 0 of the GPU run: same pools, same allocator state,
+    same q / k / v."""
+    import oracle
+
+    Hq, Hkv, D, pool, n0 = 32, 8, 128, 2048, 8192
+    ref = oracle.Manager(with_pool=True)
+    ref.init_layer(0, Hkv, D)
+    ref.reserve_layer(0, pool)
+    for which, perm in ((0, synth.shuffled(seed, pool)), (1, synth.shuffled(seed + 1, pool))):
+        p = ref.pool(0, which)
+        for _ in range(pool):
+            p.alloc()
+        for b in perm[::-1]:
+            p.free(int(b))
+    ref.append_kv_pages(0, n0)
+    ref.pool_array(0, 0)[:] = mgr.read_pool(0, 0)
+    ref.pool_array(0, 1)[:] = mgr.read_pool(0, 1)
+    q = synth.normal_bf16(seed + 300, (1, Hq, 1, D))
+    k = synth.normal_bf16(seed + 400, (1, Hkv, 1, D))
+    v = synth.normal_bf16(seed + 500, (1, Hkv, 1, D))
+    times, nbytes = [], 0
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < args.cpu_seconds or len(times) < 3:
+        t0 = time.perf_counter()
+        ref.paged_attention(0, q, k, v, Hq // Hkv, 1.0 / np.sqrt(D))
+        times.append(time.perf_counter() - t0)
+        nbytes += decode_step_bytes(ref.num_cached(0))
+    total = sum(times)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(nbytes / total / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} op steps (append 1 token + attend over {n0 + 1}..{ref.num_cached(0)} keys, "
+                      f"Qwen3-4B shape) of the oracle restatement, gcc -O3 -mavx2 -mfma -mf16c, 1 thread",
+            "us_per_step_median": round(1e6 * statistics.median(times), 1),
+            "host_cores": os.cpu_count(), "cpu_model": cpu_model}
+
+
+if __name__ == "__main__":
+    main()

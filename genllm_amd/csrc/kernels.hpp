@@ -60,9 +60,8 @@ struct AttnParams {
     int32_t causal = 1;
     int64_t page_elems = 0;
     int64_t kv_row = 0;       // elements between consecutive tokens in a page (Hkv * D)
-    // split-K decode
+    // split-K decode: per-split partials [unit][split][row][D] then {m, l} per (unit, split, row)
     float* partial = nullptr;
-    int32_t* counters = nullptr;
     int32_t pages_per_split = 0, n_splits = 1, n_chunks = 1;
 };
 

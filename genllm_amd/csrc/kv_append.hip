@@ -5,8 +5,11 @@
 //   ApplyRopeImpl<CPU> src/backend/cpu/rope.cpp:76-119
 //   append_kv_from_tensor src/core/page_attention.cpp:104-140
 //
-// Work split: one wave per task, a task = 8 rows (heads) of one token and one
-// kind (q rows, k rows or v rows).  Row r of the task sits on lanes 8r..8r+7.
+// Work split: a task = 8 rows (heads) of one token and one kind (q, k or v
+// rows); row r of a task sits on lanes 8r..8r+7.  Tasks are numbered kind by
+// kind, and each wave takes TPW consecutive tasks of one kind, issuing the
+// loads of all of them before any arithmetic so that a wave keeps TPW * 2 KiB
+// of reads in flight.
 //
 // K/q lanes: lane j of a row holds elements 4j + 32t + {0,1,2,3}, t = 0..D/32-1
 // (one 8-byte load per t).  That puts the CPU rms_norm's 32 running sums
@@ -33,20 +36,30 @@ namespace genllm {
 
 #pragma clang fp contract(off)
 
+namespace {
+
+constexpr int TPW = 4;  // tasks per wave
+
 template <int D>
-struct AppendKernel {
-    static constexpr int R = D / 32;   // rounds of 32 elements
-    static constexpr int U = D / 64;   // 16-byte V chunks per lane
+struct Append {
+    static constexpr int R = D / 32;  // 8-byte chunks per q/k row and lane
+    static constexpr int U = D / 64;  // 16-byte chunks per v row and lane
 
     __device__ static int32_t page_id(const AppendParams& p, int lp, int which) {
-        int rel = lp - p.upd.first;
+        const int rel = lp - p.upd.first;
         if (rel >= 0 && rel < p.upd.count) return which ? p.upd.v[rel] : p.upd.k[rel];
         return which ? p.v_ids[lp] : p.k_ids[lp];
     }
 
-    // Norm (optional) + RoPE (optional) of one row held as R pairs-of-pairs.
-    __device__ static void norm_rope_row(uint2 (&x)[R], const float* gamma, float eps, const float* cos_row,
-                                         const float* sin_row, int j, bool do_norm) {
+    __device__ static uint16_t* k_dst(const AppendParams& p, int tok, int h) {
+        const int gpos = p.pos0 + tok;
+        const int64_t id = page_id(p, gpos / kPage, 0);
+        return p.k_pool + id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + h * D;
+    }
+
+    // RMSNorm (optional) + RoPE (optional) of one row, in place.
+    __device__ static void norm_rope(uint2 (&x)[R], const float* gamma, float eps, const float* cos_row,
+                                     const float* sin_row, int j) {
         float v[R][4];
 #pragma unroll
         for (int t = 0; t < R; ++t) {
@@ -55,7 +68,7 @@ struct AppendKernel {
             v[t][2] = bf16_lo(x[t].y);
             v[t][3] = bf16_hi(x[t].y);
         }
-        if (do_norm) {
+        if (gamma) {
             float A[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -64,26 +77,23 @@ struct AppendKernel {
                 for (int t = 0; t < R; ++t) a = __builtin_fmaf(v[t][q], v[t][q], a);
                 A[q] = a;
             }
-            // A[k]+A[8+k] (lanes j, j+2) then +(A[16+k]+A[24+k]) (lanes j+4, j+6)
-            float X[4], T[4];
+            float X[4], T[4], u[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) X[q] = A[q] + __shfl_down(A[q], 2, 8);
+            for (int q = 0; q < 4; ++q) X[q] = A[q] + __shfl_down(A[q], 2, 8);  // A[k] + A[8+k]
 #pragma unroll
-            for (int q = 0; q < 4; ++q) T[q] = X[q] + __shfl_down(X[q], 4, 8);
-            // lane 0: T[0..3], lane 1: T[4..7]; u[i] = T[i] + T[i+4]
-            float u[4];
+            for (int q = 0; q < 4; ++q) T[q] = X[q] + __shfl_down(X[q], 4, 8);  // + (A[16+k] + A[24+k])
 #pragma unroll
-            for (int q = 0; q < 4; ++q) u[q] = T[q] + __shfl_down(T[q], 1, 8);
+            for (int q = 0; q < 4; ++q) u[q] = T[q] + __shfl_down(T[q], 1, 8);  // T[i] + T[i+4]
             float ss = (u[0] + u[1]) + (u[2] + u[3]);
             ss = __shfl(ss, 0, 8);
-            float r = 1.0f / __builtin_sqrtf(ss / float(D) + eps);
+            const float r = 1.0f / __builtin_sqrtf(ss / float(D) + eps);
 #pragma unroll
             for (int t = 0; t < R; ++t) {
-                float4 g = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * t);
-                float gv[4] = {g.x, g.y, g.z, g.w};
+                const float4 gw = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * t);
+                const float gv[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    float y = (v[t][q] * r) * gv[q];
+                    const float y = (v[t][q] * r) * gv[q];
                     v[t][q] = __uint_as_float(__float_as_uint(y) & 0xFFFF0000u);  // truncating store
                 }
             }
@@ -92,17 +102,15 @@ struct AppendKernel {
         if (cos_row) {
 #pragma unroll
             for (int t = 0; t < R / 2; ++t) {
-                float4 c4 = *reinterpret_cast<const float4*>(cos_row + 4 * j + 32 * t);
-                float4 s4 = *reinterpret_cast<const float4*>(sin_row + 4 * j + 32 * t);
-                float c[4] = {c4.x, c4.y, c4.z, c4.w};
-                float s[4] = {s4.x, s4.y, s4.z, s4.w};
+                const float4 c4 = *reinterpret_cast<const float4*>(cos_row + 4 * j + 32 * t);
+                const float4 s4 = *reinterpret_cast<const float4*>(sin_row + 4 * j + 32 * t);
+                const float c[4] = {c4.x, c4.y, c4.z, c4.w};
+                const float s[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    float x0 = v[t][q], x1 = v[t + R / 2][q];
-                    float y0 = __builtin_fmaf(x0, c[q], -(x1 * s[q]));
-                    float y1 = __builtin_fmaf(x0, s[q], x1 * c[q]);
-                    o[t][q] = f32_to_bf16_ref(y0);
-                    o[t + R / 2][q] = f32_to_bf16_ref(y1);
+                    const float x0 = v[t][q], x1 = v[t + R / 2][q];
+                    o[t][q] = f32_to_bf16_ref(__builtin_fmaf(x0, c[q], -(x1 * s[q])));
+                    o[t + R / 2][q] = f32_to_bf16_ref(__builtin_fmaf(x0, s[q], x1 * c[q]));
                 }
             }
         } else {
@@ -120,78 +128,106 @@ struct AppendKernel {
 
     __device__ static void run(const AppendParams& p) {
         const int lane = threadIdx.x & 63;
-        const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
         const int r = lane >> 3, j = lane & 7;
-
         if (blockIdx.x == 0 && threadIdx.x < p.upd.count) {
             p.k_ids[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
             p.v_ids[p.upd.first + threadIdx.x] = p.upd.v[threadIdx.x];
         }
-        const int T = p.nq_tasks + 2 * p.nkv_tasks;
-        const int tok = wave / T;
-        if (tok >= p.S) return;
-        const int kind = wave - tok * T;
+        // wave -> (kind, first task of the kind)
+        const int ngq = p.nq_tasks, ngk = p.nkv_tasks;
+        const int64_t nq = int64_t(p.S) * ngq, nk = int64_t(p.S) * ngk;
+        const int64_t wq = (nq + TPW - 1) / TPW, wk = (nk + TPW - 1) / TPW;
+        int64_t w = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+        int kind;
+        int64_t t0, n_kind;
+        int ng;
+        if (w < wq) {
+            kind = 0, t0 = w * TPW, n_kind = nq, ng = ngq;
+        } else if (w < wq + wk) {
+            kind = 1, t0 = (w - wq) * TPW, n_kind = nk, ng = ngk;
+        } else {
+            kind = 2, t0 = (w - wq - wk) * TPW, n_kind = nk, ng = ngk;
+            if (t0 >= n_kind) return;
+        }
 
-        if (kind < p.nq_tasks + p.nkv_tasks) {
-            // q or k rows: norm + RoPE
-            const bool is_q = kind < p.nq_tasks;
-            const int h = (is_q ? kind : kind - p.nq_tasks) * 8 + r;
+        if (kind < 2) {
+            const bool is_q = kind == 0;
             const int H = is_q ? p.Hq : p.Hkv;
-            if (h >= H) return;
-            const uint16_t* src = is_q ? p.q + tok * p.q_tok_stride + h * p.q_head_stride
-                                       : p.k + tok * p.k_tok_stride + h * p.k_head_stride;
-            uint2 x[R];
+            uint2 x[TPW][R];
+            int tok[TPW], h[TPW];
+            bool ok[TPW];
 #pragma unroll
-            for (int t = 0; t < R; ++t) x[t] = *reinterpret_cast<const uint2*>(src + 4 * j + 32 * t);
+            for (int u = 0; u < TPW; ++u) {
+                const int64_t t = t0 + u;
+                tok[u] = int(t / ng);
+                h[u] = int(t - int64_t(tok[u]) * ng) * 8 + r;
+                ok[u] = t < n_kind && h[u] < H;
+                const uint16_t* src = is_q ? p.q + tok[u] * p.q_tok_stride + h[u] * p.q_head_stride
+                                           : p.k + tok[u] * p.k_tok_stride + h[u] * p.k_head_stride;
+#pragma unroll
+                for (int c = 0; c < R; ++c)
+                    x[u][c] = ok[u] ? *reinterpret_cast<const uint2*>(src + 4 * j + 32 * c) : make_uint2(0, 0);
+            }
             const float* gamma = is_q ? p.gamma_q : p.gamma_k;
-            const float* crow = p.cos_tab ? p.cos_tab + (p.rope_pos0 + tok) * p.rope_stride : nullptr;
-            const float* srow = p.sin_tab ? p.sin_tab + (p.rope_pos0 + tok) * p.rope_stride : nullptr;
-            norm_rope_row(x, gamma, p.eps, crow, srow, j, gamma != nullptr);
-            uint16_t* dst;
-            if (is_q) {
-                dst = p.q_out + tok * p.qo_tok_stride + h * p.qo_head_stride;
-            } else {
-                const int g = p.pos0 + tok;
-                const int32_t id = page_id(p, g / kPage, 0);
-                dst = p.k_pool + int64_t(id) * p.page_elems + int64_t(g % kPage) * p.Hkv * D + h * D;
+#pragma unroll
+            for (int u = 0; u < TPW; ++u) {
+                if (t0 + u >= n_kind) break;  // wave-uniform
+                const float* crow = p.cos_tab ? p.cos_tab + (p.rope_pos0 + tok[u]) * p.rope_stride : nullptr;
+                const float* srow = p.sin_tab ? p.sin_tab + (p.rope_pos0 + tok[u]) * p.rope_stride : nullptr;
+                norm_rope(x[u], gamma, p.eps, crow, srow, j);
+                if (!ok[u]) continue;
+                uint16_t* dst = is_q ? p.q_out + tok[u] * p.qo_tok_stride + h[u] * p.qo_head_stride
+                                     : k_dst(p, tok[u], h[u]);
+#pragma unroll
+                for (int c = 0; c < R; ++c) *reinterpret_cast<uint2*>(dst + 4 * j + 32 * c) = x[u][c];
+            }
+        } else {
+            uint4 x[TPW][U];
+            uint16_t* dst[TPW];
+#pragma unroll
+            for (int u = 0; u < TPW; ++u) {
+                const int64_t t = t0 + u;
+                const int tk = int(t / ng);
+                const int hh = int(t - int64_t(tk) * ng) * 8 + r;
+                const bool ok = t < n_kind && hh < p.Hkv;
+                dst[u] = nullptr;
+                if (ok) {
+                    const uint16_t* src = p.v + tk * p.v_tok_stride + hh * p.v_head_stride;
+#pragma unroll
+                    for (int c = 0; c < U; ++c) x[u][c] = *reinterpret_cast<const uint4*>(src + 8 * j + 64 * c);
+                    const int gpos = p.pos0 + tk;
+                    const int64_t id = page_id(p, gpos / kPage, 1);
+                    dst[u] = p.v_pool + id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + hh * D;
+                }
             }
 #pragma unroll
-            for (int t = 0; t < R; ++t) *reinterpret_cast<uint2*>(dst + 4 * j + 32 * t) = x[t];
-        } else {
-            // v rows: plain copy
-            const int h = (kind - p.nq_tasks - p.nkv_tasks) * 8 + r;
-            if (h >= p.Hkv) return;
-            const uint16_t* src = p.v + tok * p.v_tok_stride + h * p.v_head_stride;
-            const int g = p.pos0 + tok;
-            const int32_t id = page_id(p, g / kPage, 1);
-            uint16_t* dst = p.v_pool + int64_t(id) * p.page_elems + int64_t(g % kPage) * p.Hkv * D + h * D;
-            uint4 x[U];
+            for (int u = 0; u < TPW; ++u)
+                if (dst[u])
 #pragma unroll
-            for (int u = 0; u < U; ++u) x[u] = *reinterpret_cast<const uint4*>(src + 8 * j + 64 * u);
-#pragma unroll
-            for (int u = 0; u < U; ++u) *reinterpret_cast<uint4*>(dst + 8 * j + 64 * u) = x[u];
+                    for (int c = 0; c < U; ++c) *reinterpret_cast<uint4*>(dst[u] + 8 * j + 64 * c) = x[u][c];
         }
     }
 };
 
 template <int D>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
-    AppendKernel<D>::run(p);
+    Append<D>::run(p);
 }
 
+}  // namespace
+
 int launch_kv_append(const AppendParams& p, int head_dim, hipStream_t stream) {
-    const int T = p.nq_tasks + 2 * p.nkv_tasks;
-    const int64_t waves = int64_t(p.S) * T;
-    const int blocks = int((waves + 3) / 4);
+    const int64_t nq = int64_t(p.S) * p.nq_tasks, nk = int64_t(p.S) * p.nkv_tasks;
+    const int64_t waves = (nq + TPW - 1) / TPW + 2 * ((nk + TPW - 1) / TPW);
+    int64_t blocks = (waves + 3) / 4;
     if (blocks <= 0) {
-        // nothing to scatter, but a table update may still be pending
         if (p.upd.count == 0) return GENLLM_OK;
+        blocks = 1;  // table update only
     }
-    const int nblk = blocks > 0 ? blocks : 1;
     switch (head_dim) {
-        case 64: hipLaunchKernelGGL(kv_append_kernel<64>, dim3(nblk), dim3(256), 0, stream, p); break;
-        case 128: hipLaunchKernelGGL(kv_append_kernel<128>, dim3(nblk), dim3(256), 0, stream, p); break;
-        case 256: hipLaunchKernelGGL(kv_append_kernel<256>, dim3(nblk), dim3(256), 0, stream, p); break;
+        case 64: hipLaunchKernelGGL(kv_append_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL(kv_append_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, stream, p); break;
+        case 256: hipLaunchKernelGGL(kv_append_kernel<256>, dim3(unsigned(blocks)), dim3(256), 0, stream, p); break;
         default: return fail(GENLLM_ERR_UNSUPPORTED, "kv append: head_dim must be 64, 128 or 256");
     }
     GENLLM_LAUNCH_CHECK("kv_append_kernel");

@@ -99,7 +99,7 @@ struct genllm_kv {
     char* base = nullptr;  // kv_cache MemoryPool buffer
     size_t capacity = 0, cursor = 0;
     std::map<int32_t, LayerState> layers;
-    void* ws = nullptr;    // split-K decode workspace (zero-filled on allocation)
+    void* ws = nullptr;    // split-K decode workspace (per-split partials)
     size_t ws_bytes = 0;
 };
 
@@ -182,7 +182,7 @@ LayerState* active_layer(genllm_kv* kv, int32_t layer) {
 }
 
 // Split-K workspace sized for the layer's max_blocks, grown when a wider query
-// chunk needs more rows; zero-filled because the kernel's counters start at 0.
+// chunk needs more rows.
 int ensure_workspace(genllm_kv* kv, size_t need) {
     if (need <= kv->ws_bytes) return GENLLM_OK;
     if (kv->ws) {
@@ -192,7 +192,6 @@ int ensure_workspace(genllm_kv* kv, size_t need) {
         kv->ws_bytes = 0;
     }
     GENLLM_HIP_TRY(hipMalloc(&kv->ws, need));
-    GENLLM_HIP_TRY(hipMemset(kv->ws, 0, need));
     kv->ws_bytes = need;
     return GENLLM_OK;
 }
@@ -214,14 +213,13 @@ int check_attn_args(const AttnParams& p, int head_dim) {
 }
 
 // Short query chunks (<= 16 rows per kv head) take the split-K decode kernel,
-// with the manager's workspace sized for the layer's largest table (a split
-// holds at least 4 pages unless GENLLM_DECODE_PPS asks for fewer); longer
-// chunks take the MFMA prefill kernel.
+// with the manager's workspace sized for the most splits the layer's largest
+// table can need; longer chunks take the MFMA prefill kernel.
 int run_attention(AttnParams p, int head_dim, int32_t max_blocks, hipStream_t stream, genllm_kv* kv) {
     if (int rc = check_attn_args(p, head_dim)) return rc;
     if (p.G * p.S <= 16) {
         const int ws_pages = std::max(p.n_pages, max_blocks);
-        const size_t need = decode_workspace_bytes(p.Hq, p.Hkv, p.S, head_dim, std::max(1, (ws_pages + 3) / 4));
+        const size_t need = decode_workspace_bytes(p.Hq, p.Hkv, p.S, head_dim, ws_pages);
         if (int rc = ensure_workspace(kv, need)) return rc;
         if (int rc = decode_plan(p, head_dim, kv->ws_bytes, kv->ws)) return rc;
         return launch_paged_decode(p, head_dim, stream);

@@ -1,31 +1,41 @@
-// paged_decode.hip -- split-K paged decode attention for GQA, one launch.
+// paged_decode.hip -- split-K paged decode attention for GQA.
 //
 // Computes the attention loop of PagedAttentionImpl<CPU>::execute
 // (src/backend/cpu/attention.cpp:148-215) for short query chunks:
 //   out[q] = sum_t softmax_t(scale * q.k_t) v_t over keys t <= q_abs (causal)
 // with kv head h = q head / groups (:158) and q_abs = n_cached - S + s (:164).
 //
-// Grid (splits, Hkv, row chunks), 256 threads = 4 waves.  A workgroup owns one
-// kv head and a contiguous range of pages; its 4 waves take pages round-robin.
-// Rows = the (query, q-head) pairs of the kv head, 4 per chunk, so the K/V of a
-// kv head is read once for all its GQA q heads.
+// Split kernel: grid (splits, Hkv), 256 threads = 4 waves.  A workgroup owns
+// one kv head and a contiguous range of pages; its waves take pages
+// round-robin.  The rows of the kv head -- its (query, GQA q-head) pairs, at
+// most 16 -- are the 16 columns of the MFMA tiles, so K/V are read once for all
+// of them.
 //
-// Per page (16 tokens) and wave:
-//   S = Q K^T on v_mfma_f32_16x16x32_bf16: A = Q (rows 0..3 real, 4..15 zero),
-//     B = K^T read straight from the page: lane l loads token l%16, dims
-//     32c + 8(l/16) .. +7 (16 B; 64 contiguous bytes per token row per load).
-//     D[m][n] lands in lane n + 16(m/4), register m%4, so lanes 0..15 hold the
-//     4 rows of token l.
-//   softmax: 16-lane DPP max, exp2 with scale*log2(e) folded in, running
-//     (m, l) kept per lane; the row max is made wave-uniform with readfirstlane.
-//   O += P V on VALU: lane l owns dims 8(l%16)..+7 of tokens 4i + l/16
-//     (16-byte V loads, 4 token rows of 256 B per instruction); P goes through
-//     LDS as [token][row].
-// End of range: lanes and waves are reduced, the workgroup's (m, l, o) for its
-// split go to the workspace, and the last workgroup of the kv head (atomic
-// counter, agent-scope fences) merges all splits with the log-sum-exp rule
-//   M = max m_s, L = sum l_s 2^(m_s-M), O = sum o_s 2^(m_s-M), out = O * (1/L)
-// and resets the counter.  With one split the workgroup writes out directly.
+// Per page (16 tokens) and wave, on MFMA only:
+//   S^T = K Q^T  v_mfma_f32_16x16x32_bf16 x D/32: A = K straight from the page
+//        (lane l: token l%16, dims 32c+8(l/16)..+7, 16-byte loads), B = Q^T held
+//        in registers (lane l: row l%16).  D[tok][row] lands in lane row + 16g,
+//        register i = tok - 4g: each lane holds 4 keys of ONE row, so the row
+//        max is an in-lane max plus two cross-lane steps, and the running
+//        (m, l) of a row live in its lanes.
+//   O^T += V^T P^T  v_mfma_f32_16x16x16_bf16 x D/16: B = P^T is the lane's own 4
+//        probabilities (tokens 4g..4g+3 of its row) as bf16; A = V^T: each lane
+//        loads V for tokens 4g..4g+3, dims 8(l%16)..+7 (16-byte loads) and writes
+//        them to LDS transposed ([dim][token], 8-byte stores), then reads the
+//        A operand (dim l%16 of a 16-dim block, tokens 4g..4g+3) back.
+//        O^T[dim][row] is again lane-local to the row, so the rescale by
+//        2^(m_old - m_new) needs no exchange.
+// Memory-level parallelism: the wave reads the block-table entries of all its
+// pages with one load up front and keeps PF pages of K/V in flight in
+// registers (page j+PF-1 is requested before page j is computed).
+//
+// End of range: the 4 waves are merged through LDS and the workgroup's
+// (m, l, o) per row go to the workspace; a second kernel merges the splits with
+// the log-sum-exp rule  M = max m_s, L = sum l_s 2^(m_s-M),
+// O = sum o_s 2^(m_s-M), out = O * (1/L).  With one split the workgroup writes
+// the output directly.  (A single launch in which the last workgroup merges
+// needs agent-scope fences -- an L2 write-back and invalidate per workgroup on
+// gfx950 -- and measured slower.)
 #include <cfloat>
 
 #include "common.hpp"
@@ -34,256 +44,313 @@
 namespace genllm {
 
 namespace {
-constexpr int kRows = 4;     // q rows per chunk
+constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
 constexpr int kWaves = 4;
+constexpr int kMaxSplits = 256;
+constexpr int PF = 4;          // pages in flight per wave
+constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
 
-__device__ __forceinline__ float uniform(float x) {
-    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma16x16x16(const s16x4_t& a, const s16x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
+
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+    const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
+    return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+struct PageRegs {
+    uint4 k[4];  // K^T operand chunks (D = 128)
+    uint4 v[4];  // V rows of tokens 4g..4g+3
+};
 
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
     static_assert(D == 128, "decode kernel: head_dim 128");
-    constexpr int KS = D / 32;     // MFMA k-steps
-    constexpr int PART = D + 2;    // o[D], m, l
+    constexpr int KS = D / 32;  // S^T k-steps
+    constexpr int DB = D / 16;  // O^T dim blocks
 
-    __shared__ float4 lds_p[kWaves][kPage];           // p[token][row]
+    __shared__ __attribute__((aligned(16))) uint16_t lds_vt[kWaves][D * VT_ROW];
     __shared__ float lds_m[kWaves][kRows], lds_l[kWaves][kRows];
-    __shared__ float lds_o[kWaves][kRows][D];
-    __shared__ int s_last;
+    __shared__ float lds_o[kWaves][kRows][D + 4];
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n16 = lane & 15, g = lane >> 4;
-    const int sp = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
-    const int rows_total = p.G * p.S;
+    const int sp = blockIdx.x, h = blockIdx.y;
+    const int rows_total = p.G * p.S;  // <= 16
 
-    // Q operand: row m = n16 (only 0..3 are real), k-slice of lane group g.
-    bf16x8_t qa[KS];
+    // this lane's row (MFMA column): q head h*G + r%G, query r/G
+    const int r = n16;
+    const bool row_ok = r < rows_total;
+    const int qabs = p.causal ? p.n_cached - p.S + r / p.G : p.n_cached - 1;
+    bf16x8_t qb[KS];
     {
-        const int R = z * kRows + n16;
-        const bool ok = n16 < kRows && R < rows_total;
-        const uint16_t* qrow = p.q;
-        if (ok) qrow = p.q + int64_t(h * p.G + R % p.G) * p.q_head_stride + int64_t(R / p.G) * p.q_tok_stride;
+        const uint16_t* qrow = p.q + int64_t(h * p.G + r % p.G) * p.q_head_stride + int64_t(r / p.G) * p.q_tok_stride;
 #pragma unroll
         for (int c = 0; c < KS; ++c) {
             uint4 u = make_uint4(0, 0, 0, 0);
-            if (ok) u = *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g);
-            qa[c] = as_bf16x8(u);
+            if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g);
+            qb[c] = as_bf16x8(u);
         }
-    }
-    int qabs[kRows];
-    bool rvalid[kRows];
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-        const int R = z * kRows + i;
-        rvalid[i] = R < rows_total;
-        qabs[i] = p.causal ? p.n_cached - p.S + R / p.G : p.n_cached - 1;
     }
 
     const int begin = sp * p.pages_per_split;
     const int end = min(begin + p.pages_per_split, p.n_pages);
-    const int last_page = (p.n_cached - 1) / kPage;
-
-    float m_run[kRows], l_run[kRows], o[kRows][8];
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-        m_run[i] = -INFINITY;
-        l_run[i] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 8; ++d) o[i][d] = 0.0f;
+    const int np = end - begin - wv > 0 ? (end - begin - wv + kWaves - 1) / kWaves : 0;
+    int my_kid = 0, my_vid = 0;  // block-table entries of the wave's pages, one per lane
+    if (lane < np) {
+        my_kid = p.k_ids[begin + wv + kWaves * lane];
+        my_vid = p.v_ids[begin + wv + kWaves * lane];
     }
+    const uint16_t* kcol = p.k_pool + h * D + n16 * p.kv_row + 8 * g;
+    const uint16_t* vcol = p.v_pool + h * D + (4 * g) * p.kv_row + 8 * n16;
+    uint16_t* vt = lds_vt[wv];
 
-    for (int pg = begin + wv; pg < end; pg += kWaves) {
-        const int64_t kid = p.k_ids[pg], vid = p.v_ids[pg];
-        const uint16_t* kbase = p.k_pool + kid * p.page_elems + h * D;
-        const uint16_t* vbase = p.v_pool + vid * p.page_elems + h * D;
-        uint4 kb[KS], vv[4];
+    auto load_page = [&](int j, PageRegs& pr) {
+        const int64_t kid = __builtin_amdgcn_readlane(my_kid, j);
+        const int64_t vid = __builtin_amdgcn_readlane(my_vid, j);
+        const uint16_t* kb = kcol + kid * p.page_elems;
+        const uint16_t* vb = vcol + vid * p.page_elems;
 #pragma unroll
-        for (int c = 0; c < KS; ++c)
-            kb[c] = *reinterpret_cast<const uint4*>(kbase + n16 * p.kv_row + 32 * c + 8 * g);
+        for (int c = 0; c < KS; ++c) pr.k[c] = *reinterpret_cast<const uint4*>(kb + 32 * c);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            vv[i] = *reinterpret_cast<const uint4*>(vbase + (4 * i + g) * p.kv_row + 8 * n16);
+        for (int i = 0; i < 4; ++i) pr.v[i] = *reinterpret_cast<const uint4*>(vb + i * p.kv_row);
+    };
 
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4_t acc[DB];
 #pragma unroll
-        for (int c = 0; c < KS; ++c) acc = mfma16x16x32(qa[c], as_bf16x8(kb[c]), acc);
+    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-        const int tok = pg * kPage + n16;
-        float s[kRows], mx[kRows];
-#pragma unroll
-        for (int i = 0; i < kRows; ++i) {
-            const bool ok = rvalid[i] && tok < p.n_cached && tok <= qabs[i];
-            s[i] = ok ? acc[i] * p.scale_log2 : -INFINITY;
-            mx[i] = uniform(row16_max(s[i]));
-        }
-        float alpha[kRows], pr[kRows];
-#pragma unroll
-        for (int i = 0; i < kRows; ++i) {
-            const float mn = fmaxf(m_run[i], mx[i]);
-            const float mu = mn == -INFINITY ? 0.0f : mn;
-            alpha[i] = exp2_fast(m_run[i] - mu);
-            pr[i] = exp2_fast(s[i] - mu);
-            l_run[i] = l_run[i] * alpha[i] + pr[i];
-            m_run[i] = mn;
-        }
-        if (g == 0) lds_p[wv][n16] = make_float4(pr[0], pr[1], pr[2], pr[3]);
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int i = 0; i < kRows; ++i)
-#pragma unroll
-            for (int d = 0; d < 8; ++d) o[i][d] *= alpha[i];
-        const bool tail = pg == last_page;
+    auto compute_page = [&](int j, const PageRegs& pr) {
+        const int pg = begin + wv + kWaves * j;
+        const int tok0 = pg * kPage + 4 * g;  // this lane's 4 keys: tok0 .. tok0+3
+        // V^T into LDS first (its latency hides behind the S^T MFMAs)
+        uint4 v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = 4 * i + g;
-            const float4 pp = lds_p[wv][t];
-            uint4 u = vv[i];
-            if (tail && pg * kPage + t >= p.n_cached) u = make_uint4(0, 0, 0, 0);  // unfilled slots
-            const float v[8] = {bf16_lo(u.x), bf16_hi(u.x), bf16_lo(u.y), bf16_hi(u.y),
-                                bf16_lo(u.z), bf16_hi(u.z), bf16_lo(u.w), bf16_hi(u.w)};
-            const float pw[4] = {pp.x, pp.y, pp.z, pp.w};
+            v[i] = pr.v[i];
+            if (tok0 + i >= p.n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots of the last page
+        }
+        const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
+                                  {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
 #pragma unroll
-            for (int r = 0; r < kRows; ++r)
+        for (int e = 0; e < 4; ++e) {  // dims 8*n16 + 2e (low halves) and + 2e + 1 (high halves)
+            const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][e], w[0][e], 0x05040100u),
+                                        __builtin_amdgcn_perm(w[3][e], w[2][e], 0x05040100u));
+            const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][e], w[0][e], 0x07060302u),
+                                        __builtin_amdgcn_perm(w[3][e], w[2][e], 0x07060302u));
+            *reinterpret_cast<uint2*>(&vt[(8 * n16 + 2 * e) * VT_ROW + 4 * g]) = lo;
+            *reinterpret_cast<uint2*>(&vt[(8 * n16 + 2 * e + 1) * VT_ROW + 4 * g]) = hi;
+        }
+        // S^T = K Q^T
+        f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int d = 0; d < 8; ++d) o[r][d] = __builtin_fmaf(pw[r], v[d], o[r][d]);
+        for (int c = 0; c < KS; ++c) s = mfma16x16x32(as_bf16x8(pr.k[c]), qb[c], s);
+        float x[4], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = tok0 + i;
+            x[i] = (row_ok && t < p.n_cached && t <= qabs) ? s[i] * p.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, x[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // Lazy rescale: the row's reference max m_run only moves (and o, l are
+        // rescaled) when the page max exceeds it by more than 2^8, so p <= 256.
+        const bool grow = mx > m_run + 8.0f;
+        if (__any(grow)) {
+            const float mn = grow ? mx : m_run;
+            const float alpha = grow ? exp2_fast(m_run - mn) : 1.0f;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+            m_run = mn;
+        }
+        const float mu = m_run == -INFINITY ? 0.0f : m_run;
+        float pw[4], sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pw[i] = exp2_fast(x[i] - mu);
+            sum += pw[i];
+        }
+        l_run += sum;
+        const s16x4_t pb =
+            __builtin_bit_cast(s16x4_t, make_uint2(bf16x2_rne(pw[0], pw[1]), bf16x2_rne(pw[2], pw[3])));
+        __builtin_amdgcn_wave_barrier();
+        // O^T += V^T P^T
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const s16x4_t a =
+                __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(&vt[(16 * db + n16) * VT_ROW + 4 * g]));
+            acc[db] = mfma16x16x16(a, pb, acc[db]);
         }
         __builtin_amdgcn_wave_barrier();
+    };
+
+    PageRegs buf[PF];
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u)
+        if (u < np) load_page(u, buf[u]);
+    for (int j0 = 0; j0 < np; j0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int j = j0 + u;
+            if (j < np) {
+                if (j + PF - 1 < np) load_page(j + PF - 1, buf[(u + PF - 1) % PF]);
+                compute_page(j, buf[u]);
+            }
+        }
     }
 
-    // lane reductions: l over the 16 token lanes, o over the 4 token groups
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-        l_run[i] = row16_sum(l_run[i]);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            o[i][d] += __shfl_xor(o[i][d], 16);
-            o[i][d] += __shfl_xor(o[i][d], 32);
-        }
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < kRows; ++i) {
-            lds_m[wv][i] = m_run[i];
-            lds_l[wv][i] = l_run[i];
-        }
-    }
+    // l over the 4 lane groups of the row; o is already complete per lane
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
     if (g == 0) {
-#pragma unroll
-        for (int i = 0; i < kRows; ++i)
-#pragma unroll
-            for (int d = 0; d < 8; ++d) lds_o[wv][i][8 * n16 + d] = o[i][d];
+        lds_m[wv][n16] = m_run;
+        lds_l[wv][n16] = l_run;
     }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_o[wv][n16][16 * db + 4 * g + i] = acc[db][i];
     __syncthreads();
 
-    // workgroup merge: thread -> (row i, dims d2, d2+1)
-    const int i = threadIdx.x >> 6;
-    const int d2 = (threadIdx.x & 63) * 2;
-    float M = -INFINITY;
+    // workgroup merge: wave -> rows ri, ri+4, ...; lane -> dims d2, d2+1
+    for (int ri = wv; ri < rows_total; ri += kWaves) {
+        const int d2 = lane * 2;
+        float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds_m[w][i]);
-    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
-    if (M != -INFINITY) {
+        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_m[w2][ri]);
+        float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+        if (M != -INFINITY) {
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float e = exp2_fast(lds_m[w][i] - M);
-            L += lds_l[w][i] * e;
-            O0 += lds_o[w][i][d2] * e;
-            O1 += lds_o[w][i][d2 + 1] * e;
+            for (int w2 = 0; w2 < kWaves; ++w2) {
+                const float e = exp2_fast(lds_m[w2][ri] - M);
+                L += lds_l[w2][ri] * e;
+                O0 += lds_o[w2][ri][d2] * e;
+                O1 += lds_o[w2][ri][d2 + 1] * e;
+            }
         }
-    }
-    const int R = z * kRows + i;
-    const bool row_ok = R < rows_total;
-    uint16_t* orow = row_ok ? p.out + int64_t(h * p.G + R % p.G) * p.o_head_stride + int64_t(R / p.G) * p.o_tok_stride
-                            : nullptr;
-
-    if (p.n_splits == 1) {
-        if (row_ok) {
+        if (p.n_splits == 1) {
+            uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
             const float inv = 1.0f / L;
             *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(O0 * inv), f32_to_bf16_ref(O1 * inv));
+        } else {
+            // partials: o [h][split][row][D], then {m, l} [h][split][row]
+            float* po = p.partial + ((int64_t(h) * p.n_splits + sp) * rows_total + ri) * D;
+            *reinterpret_cast<float2*>(po + d2) = make_float2(O0, O1);
+            if (lane == 0) {
+                float2* ml = reinterpret_cast<float2*>(p.partial + int64_t(p.Hkv) * p.n_splits * rows_total * D);
+                ml[(int64_t(h) * p.n_splits + sp) * rows_total + ri] = make_float2(M, L);
+            }
         }
-        return;
     }
-
-    const int unit = h * p.n_chunks + z;
-    float* part = p.partial + ((int64_t(unit) * p.n_splits + sp) * kRows + i) * PART;
-    part[d2] = O0;
-    part[d2 + 1] = O1;
-    if (d2 == 0) {
-        part[D] = M;
-        part[D + 1] = L;
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int prev = atomicAdd(p.counters + unit, 1);
-        s_last = prev == p.n_splits - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    // last workgroup of this kv head: merge every split
-    M = -INFINITY;
-    L = 0.0f;
-    O0 = 0.0f;
-    O1 = 0.0f;
-    const float* base = p.partial + (int64_t(unit) * p.n_splits * kRows + i) * PART;
-    for (int s2 = 0; s2 < p.n_splits; ++s2) {
-        const float* ps = base + int64_t(s2) * kRows * PART;
-        const float ms = __builtin_nontemporal_load(ps + D);
-        const float ls = __builtin_nontemporal_load(ps + D + 1);
-        const float o0 = __builtin_nontemporal_load(ps + d2);
-        const float o1 = __builtin_nontemporal_load(ps + d2 + 1);
-        const float mn = fmaxf(M, ms);
-        if (mn == -INFINITY) continue;
-        const float a = exp2_fast(M - mn), b = exp2_fast(ms - mn);
-        L = L * a + ls * b;
-        O0 = O0 * a + o0 * b;
-        O1 = O1 * a + o1 * b;
-        M = mn;
-    }
-    if (row_ok) {
-        const float inv = 1.0f / L;
-        *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(O0 * inv), f32_to_bf16_ref(O1 * inv));
-    }
-    if (threadIdx.x == 0) p.counters[unit] = 0;
 }
 
-size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+// Merge of the splits: one workgroup per (row, kv head).  Wave w takes splits
+// w, w+4, ...; lane -> 2 dims; the waves' sums meet in LDS.
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
+    __shared__ float w_tab[kMaxSplits];
+    __shared__ float part[kWaves][D + 2];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int ri = blockIdx.x, h = blockIdx.y;
+    const int rows = p.G * p.S;
+    const int ns = p.n_splits;
+    const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
+                       int64_t(h) * ns * rows + ri;
+    // max over splits, then (wave 0) weights 2^(m_s - M) and L
+    float mx = -INFINITY;
+    for (int s2 = lane; s2 < ns; s2 += 64) mx = fmaxf(mx, ml[s2 * rows].x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (wv == 0) {
+        float lsum = 0.0f;
+        for (int s2 = lane; s2 < ns; s2 += 64) {
+            const float2 v = ml[s2 * rows];
+            const float e = (mx == -INFINITY || v.x == -INFINITY) ? 0.0f : exp2_fast(v.x - mx);
+            w_tab[s2] = e;
+            lsum += v.y * e;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+        if (lane == 0) part[0][D] = lsum;
+    }
+    __syncthreads();
+    const int d2 = lane * 2;
+    const float2* po = reinterpret_cast<const float2*>(p.partial + (int64_t(h) * ns * rows + ri) * D + d2);
+    const int64_t sstride = int64_t(rows) * D / 2;  // float2 units between splits
+    float a0 = 0.0f, a1 = 0.0f;
+    int s2 = wv;
+    for (; s2 + 3 * kWaves < ns; s2 += 4 * kWaves) {  // 4 independent loads per lane per step
+        float2 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = po[(s2 + u * kWaves) * sstride];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float wgt = w_tab[s2 + u * kWaves];
+            a0 += v[u].x * wgt;
+            a1 += v[u].y * wgt;
+        }
+    }
+    for (; s2 < ns; s2 += kWaves) {
+        const float2 v = po[s2 * sstride];
+        a0 += v.x * w_tab[s2];
+        a1 += v.y * w_tab[s2];
+    }
+    part[wv][d2] = a0;
+    part[wv][d2 + 1] = a1;
+    __syncthreads();
+    if (wv == 0) {
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+            o0 += part[w2][d2];
+            o1 += part[w2][d2 + 1];
+        }
+        const float inv = 1.0f / part[0][D];
+        uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
+        *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(o0 * inv), f32_to_bf16_ref(o1 * inv));
+    }
+}
 
 }  // namespace
 
 size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages) {
     if (Hkv <= 0 || Hq <= 0 || S <= 0 || D <= 0 || n_pages <= 0) return 0;
-    const int G = Hq / Hkv;
-    const int chunks = (G * S + kRows - 1) / kRows;
-    const size_t units = size_t(Hkv) * chunks;
-    return round_up(units * sizeof(int32_t), 256) + units * size_t(n_pages) * kRows * (D + 2) * sizeof(float);
+    const size_t rows = size_t(Hq / Hkv) * S;
+    const size_t splits = std::min<size_t>(size_t(n_pages), kMaxSplits);
+    return size_t(Hkv) * splits * rows * (D + 2) * sizeof(float);
 }
 
-// Choose pages per split: about two workgroups per CU over all kv heads and row
-// chunks.  GENLLM_DECODE_PPS overrides (tuning).
+// Pages per split: about GENLLM_DECODE_WG_PER_CU (default 1) workgroups per CU
+// over all kv heads, at most 256 splits.  GENLLM_DECODE_PPS forces the value
+// (tuning and tests).
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
-    p.n_chunks = (p.G * p.S + kRows - 1) / kRows;
-    const int64_t units = int64_t(p.Hkv) * p.n_chunks;
+    if (p.G * p.S > kRows) return fail(GENLLM_ERR_INVALID, "paged decode: seq_len * groups must be <= 16");
+    p.n_chunks = 1;
     int pps = 0;
     if (const char* e = getenv("GENLLM_DECODE_PPS")) pps = atoi(e);
     if (pps <= 0) {
-        const int64_t target = 2 * int64_t(device_cu_count());
-        pps = int((int64_t(p.n_pages) * units + target - 1) / target);
-        if (pps < 4) pps = 4;  // one page per wave at least
+        double per_cu = 1.0;
+        if (const char* e = getenv("GENLLM_DECODE_WG_PER_CU")) per_cu = atof(e);
+        const int64_t target = std::max<int64_t>(1, int64_t(per_cu * device_cu_count()));
+        pps = int((int64_t(p.n_pages) * p.Hkv + target - 1) / target);
+        if (pps < 2) pps = 2;
     }
+    pps = std::max(pps, (p.n_pages + kMaxSplits - 1) / kMaxSplits);
+    pps = std::min(pps, 64 * kWaves);  // a wave holds the ids of at most 64 pages
     p.pages_per_split = pps;
     p.n_splits = (p.n_pages + pps - 1) / pps;
     if (p.n_splits > 1) {
-        const size_t cnt_bytes = round_up(size_t(units) * sizeof(int32_t), 256);
-        const size_t need = cnt_bytes + size_t(units) * p.n_splits * kRows * (D + 2) * sizeof(float);
+        const size_t need = size_t(p.Hkv) * p.n_splits * (p.G * p.S) * (D + 2) * sizeof(float);
         if (!ws || ws_bytes < need)
             return fail(GENLLM_ERR_INVALID, "paged decode: workspace too small (need " + std::to_string(need) +
                                                 " bytes, have " + std::to_string(ws_bytes) + ")");
-        p.counters = reinterpret_cast<int32_t*>(ws);
-        p.partial = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + cnt_bytes);
+        p.partial = static_cast<float*>(ws);
     }
     return GENLLM_OK;
 }
@@ -291,9 +358,14 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged decode: head_dim must be 128");
     if (p.n_pages <= 0) return GENLLM_OK;
-    dim3 grid(p.n_splits, p.Hkv, p.n_chunks);
-    hipLaunchKernelGGL(paged_decode_kernel<128>, grid, dim3(256), 0, stream, p);
+    if (p.n_splits > kMaxSplits || p.pages_per_split > 64 * kWaves || p.G * p.S > kRows)
+        return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
+    hipLaunchKernelGGL(paged_decode_kernel<128>, dim3(p.n_splits, p.Hkv), dim3(256), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
+    if (p.n_splits > 1) {
+        hipLaunchKernelGGL(paged_decode_merge_kernel<128>, dim3(p.G * p.S, p.Hkv), dim3(256), 0, stream, p);
+        GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
+    }
     return GENLLM_OK;
 }
 

@@ -49,8 +49,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     constexpr int NT = WAVES * 64;
     constexpr int QT = QW * WAVES;
 
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[KT * KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * VROW];
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * KT * KROW];  // two buffers
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * D * VROW];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n16 = lane & 15, g = lane >> 4;
@@ -89,47 +89,94 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     const int w_last_abs = qabs0 + min(q0 + QW, p.S) - 1;
     const int w_first_abs = qabs0 + q0;
 
+    // Pipeline (one barrier per tile, two LDS buffers):
+    //   iteration t: store tile t+1 (already in registers) into buffer (t+1)&1,
+    //   request tile t+2 from HBM into registers using its block-table entries
+    //   (fetched one iteration earlier), fetch the entries of tile t+3, then
+    //   compute tile t from buffer t&1.
+    // Thread -> data: K chunk e of a tile is token 16e + tid/16 (page e of the
+    // tile), dims 8*(tid%16)..+7; V task e is the token pair 2*(tid%32), +1
+    // (page (tid%32)/8), dims 8*(tid/32 + 8e)..+7.  Lanes 0..3 of every wave
+    // hold the tile's 4 K page ids, lanes 4..7 its 4 V page ids.
+    constexpr int KCH = KT * (D / 8) / NT;          // 16-byte K chunks per thread
+    constexpr int VTK = (KT / 2) * (D / 8) / NT;    // V token-pair tasks per thread
+    static_assert(KCH * NT == KT * (D / 8) && VTK * NT == (KT / 2) * (D / 8), "tile split");
+    static_assert(NT % (KT / 2) == 0 && (NT / (D / 8)) * KCH == KT && KCH == KT / kPage, "thread map");
+    uint4 kreg[KCH], va[VTK], vb[VTK];
+    auto load_ids = [&](int tile) -> int {
+        const int page = 4 * tile + (lane & 3);
+        int id = 0;
+        if (lane < 8 && page * kPage < kv_end) id = lane < 4 ? p.k_ids[page] : p.v_ids[page];
+        return id;
+    };
+    auto load_tile = [&](int tile, int ids) {
+        const int tok0 = tile * KT;
+#pragma unroll
+        for (int e = 0; e < KCH; ++e) {
+            const int tt = 16 * e + (tid >> 4), ch = tid & 15;
+            const int pos = tok0 + tt;
+            const int64_t id = __builtin_amdgcn_readlane(ids, e);
+            kreg[e] = make_uint4(0, 0, 0, 0);
+            if (pos < p.n_cached)
+                kreg[e] = *reinterpret_cast<const uint4*>(p.k_pool + id * p.page_elems +
+                                                          int64_t(pos % kPage) * p.kv_row + hkv * D + 8 * ch);
+        }
+        const int tp = tid & (KT / 2 - 1);
+        const int64_t vid = __shfl(ids, 4 + (tp >> 3));
+#pragma unroll
+        for (int e = 0; e < VTK; ++e) {
+            const int ch = (tid >> 5) + (NT / 32) * e;
+            const int pos = tok0 + 2 * tp;
+            const uint16_t* src = p.v_pool + vid * p.page_elems + int64_t(pos % kPage) * p.kv_row + hkv * D + 8 * ch;
+            va[e] = make_uint4(0, 0, 0, 0);
+            vb[e] = make_uint4(0, 0, 0, 0);
+            if (pos < p.n_cached) va[e] = *reinterpret_cast<const uint4*>(src);
+            if (pos + 1 < p.n_cached) vb[e] = *reinterpret_cast<const uint4*>(src + p.kv_row);
+        }
+    };
+    auto store_tile = [&](int buf) {
+        uint16_t* kl = k_lds + buf * (KT * KROW);
+        uint16_t* vl = v_lds + buf * (D * VROW);
+#pragma unroll
+        for (int e = 0; e < KCH; ++e) {
+            const int tt = 16 * e + (tid >> 4), ch = tid & 15;
+            *reinterpret_cast<uint4*>(&kl[tt * KROW + 8 * ch]) = kreg[e];
+        }
+        // V transposed: the dword at V^T[d][2tp] packs tokens 2tp (low) and 2tp+1 (high)
+        const int tp = tid & (KT / 2 - 1);
+#pragma unroll
+        for (int e = 0; e < VTK; ++e) {
+            const int ch = (tid >> 5) + (NT / 32) * e;
+            const uint32_t av[4] = {va[e].x, va[e].y, va[e].z, va[e].w};
+            const uint32_t bv[4] = {vb[e].x, vb[e].y, vb[e].z, vb[e].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t* row0 = reinterpret_cast<uint32_t*>(&vl[(8 * ch + 2 * q) * VROW + 2 * tp]);
+                uint32_t* row1 = reinterpret_cast<uint32_t*>(&vl[(8 * ch + 2 * q + 1) * VROW + 2 * tp]);
+                *row0 = (av[q] & 0xFFFFu) | (bv[q] << 16);
+                *row1 = (av[q] >> 16) | (bv[q] & 0xFFFF0000u);
+            }
+        }
+    };
+
+    int ids_next = 0;
+    if (n_tiles > 0) {
+        load_tile(0, load_ids(0));
+        store_tile(0);
+        if (n_tiles > 1) load_tile(1, load_ids(1));
+        if (n_tiles > 2) ids_next = load_ids(2);
+    }
     for (int t = 0; t < n_tiles; ++t) {
         const int tok0 = t * KT;
-        __syncthreads();
-        // ---- K tile: 64 tokens x D dims, 16-byte chunks
-        for (int c = tid; c < KT * (D / 8); c += NT) {
-            const int tt = c / (D / 8), ch = c - tt * (D / 8);
-            const int pos = tok0 + tt;
-            uint4 u = make_uint4(0, 0, 0, 0);
-            if (pos < p.n_cached) {
-                const int64_t id = p.k_ids[pos / kPage];
-                u = *reinterpret_cast<const uint4*>(p.k_pool + id * p.page_elems + int64_t(pos % kPage) * p.kv_row +
-                                                    hkv * D + 8 * ch);
-            }
-            *reinterpret_cast<uint4*>(&k_lds[tt * KROW + 8 * ch]) = u;
+        __syncthreads();  // tile t is in LDS; nobody still reads buffer (t+1)&1
+        if (t + 1 < n_tiles) store_tile((t + 1) & 1);
+        if (t + 2 < n_tiles) {
+            load_tile(t + 2, ids_next);
+            if (t + 3 < n_tiles) ids_next = load_ids(t + 3);
         }
-        // ---- V tile, transposed: task = (token pair tp, 8-dim chunk ch)
-        for (int c = tid; c < (KT / 2) * (D / 8); c += NT) {
-            const int tp = c & (KT / 2 - 1), ch = c / (KT / 2);
-            const int pos = tok0 + 2 * tp;
-            uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-            if (pos < p.n_cached) {
-                const int64_t id = p.v_ids[pos / kPage];
-                a = *reinterpret_cast<const uint4*>(p.v_pool + id * p.page_elems + int64_t(pos % kPage) * p.kv_row +
-                                                    hkv * D + 8 * ch);
-            }
-            if (pos + 1 < p.n_cached) {
-                const int64_t id = p.v_ids[(pos + 1) / kPage];
-                b = *reinterpret_cast<const uint4*>(p.v_pool + id * p.page_elems +
-                                                    int64_t((pos + 1) % kPage) * p.kv_row + hkv * D + 8 * ch);
-            }
-            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                uint32_t* row0 = reinterpret_cast<uint32_t*>(&v_lds[(8 * ch + 2 * e) * VROW + 2 * tp]);
-                uint32_t* row1 = reinterpret_cast<uint32_t*>(&v_lds[(8 * ch + 2 * e + 1) * VROW + 2 * tp]);
-                *row0 = (av[e] & 0xFFFFu) | (bv[e] << 16);
-                *row1 = (av[e] >> 16) | (bv[e] & 0xFFFF0000u);
-            }
-        }
-        __syncthreads();
         if (!wave_has_rows || (p.causal && tok0 > w_last_abs)) continue;
+        const uint16_t* k_cur = k_lds + (t & 1) * (KT * KROW);
+        const uint16_t* v_cur = v_lds + (t & 1) * (D * VROW);
 
         // ---- S^T = K Q^T
         f32x4_t s[4][2];
@@ -142,7 +189,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) {
                 const bf16x8_t a =
-                    as_bf16x8(*reinterpret_cast<const uint4*>(&k_lds[(16 * mb + n16) * KROW + 32 * ks + 8 * g]));
+                    as_bf16x8(*reinterpret_cast<const uint4*>(&k_cur[(16 * mb + n16) * KROW + 32 * ks + 8 * g]));
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) s[mb][nb] = mfma16x16x32(a, qb[nb][ks], s[mb][nb]);
             }
@@ -205,7 +252,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
             }
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const uint16_t* vr = &v_lds[(16 * db + n16) * VROW + 32 * kt + 4 * g];
+                const uint16_t* vr = &v_cur[(16 * db + n16) * VROW + 32 * kt + 4 * g];
                 const uint2 lo = *reinterpret_cast<const uint2*>(vr);
                 const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
                 const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));

@@ -28,18 +28,31 @@ __global__ void fill_normal_kernel(uint16_t* dst, size_t n, uint64_t seed, uint6
     }
 }
 
-// One 16x16x32 bf16 MFMA with the operand layouts the kernels rely on:
-// lane l gives A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16]; D[4(l/16)+i][l%16]
-// comes back in register i.
-__global__ void selftest_mfma_kernel(const uint16_t* a, const uint16_t* b, float* c) {
+// One bf16 MFMA with the operand layouts the kernels rely on, K = 32
+// (v_mfma_f32_16x16x32_bf16) or K = 16 (v_mfma_f32_16x16x16_bf16):
+// lane l gives A[l%16][kk(l/16)..+kk-1] and B[kk(l/16)..+kk-1][l%16] with
+// kk = K/4; D[4(l/16)+i][l%16] comes back in register i.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+__global__ void selftest_mfma_kernel(const uint16_t* a, const uint16_t* b, float* c, int K) {
     const int l = threadIdx.x;
     const int r = l & 15, g = l >> 4;
-    uint4 ua = *reinterpret_cast<const uint4*>(a + r * 32 + 8 * g);
-    uint16_t bb[8];
-    for (int j = 0; j < 8; ++j) bb[j] = b[(8 * g + j) * 16 + r];
-    uint4 ub = make_uint4(pack2(bb[0], bb[1]), pack2(bb[2], bb[3]), pack2(bb[4], bb[5]), pack2(bb[6], bb[7]));
+    const int kk = K / 4;
+    uint16_t aa[8], bb[8];
+    for (int j = 0; j < kk; ++j) {
+        aa[j] = a[r * K + kk * g + j];
+        bb[j] = b[(kk * g + j) * 16 + r];
+    }
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = mfma16x16x32(as_bf16x8(ua), as_bf16x8(ub), acc);
+    if (K == 32) {
+        const uint4 ua = make_uint4(pack2(aa[0], aa[1]), pack2(aa[2], aa[3]), pack2(aa[4], aa[5]), pack2(aa[6], aa[7]));
+        const uint4 ub = make_uint4(pack2(bb[0], bb[1]), pack2(bb[2], bb[3]), pack2(bb[4], bb[5]), pack2(bb[6], bb[7]));
+        acc = mfma16x16x32(as_bf16x8(ua), as_bf16x8(ub), acc);
+    } else {
+        const s16x4_t sa = __builtin_bit_cast(s16x4_t, make_uint2(pack2(aa[0], aa[1]), pack2(aa[2], aa[3])));
+        const s16x4_t sb = __builtin_bit_cast(s16x4_t, make_uint2(pack2(bb[0], bb[1]), pack2(bb[2], bb[3])));
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(sa, sb, acc, 0, 0, 0);
+    }
     for (int i = 0; i < 4; ++i) c[(4 * g + i) * 16 + r] = acc[i];
 }
 
@@ -57,10 +70,11 @@ extern "C" int genllm_fill_normal_bf16(void* dst, size_t n, uint64_t seed, uint6
     return GENLLM_OK;
 }
 
-extern "C" int genllm_selftest_mfma(const void* a, const void* b, float* c, void* stream) {
+extern "C" int genllm_selftest_mfma(int32_t k, const void* a, const void* b, float* c, void* stream) {
     if (!a || !b || !c) return fail(GENLLM_ERR_INVALID, "selftest_mfma: null pointer");
+    if (k != 16 && k != 32) return fail(GENLLM_ERR_INVALID, "selftest_mfma: k must be 16 or 32");
     hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, as_stream(stream),
-                       static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), c);
+                       static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b), c, int(k));
     GENLLM_LAUNCH_CHECK("selftest_mfma_kernel");
     return GENLLM_OK;
 }

@@ -287,7 +287,8 @@ def fill_normal_bf16(t: torch.Tensor, seed: int, offset: int = 0, stream=None):
 
 
 def selftest_mfma(a, b, c, stream=None):
-    call("genllm_selftest_mfma", _ptr(a), _ptr(b), _ptr(c), _stream(stream))
+    """a [16][k], b [k][16] bf16 (k = 32 or 16) -> c [16][16] fp32 via one MFMA."""
+    call("genllm_selftest_mfma", a.shape[1], _ptr(a), _ptr(b), _ptr(c), _stream(stream))
 
 
 # ------------------------------------------------------------- conversions

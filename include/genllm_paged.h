@@ -157,17 +157,15 @@ int genllm_kv_scatter(const void *k, int64_t k_tok_stride, int64_t k_head_stride
                       const int32_t *k_ids, const int32_t *v_ids, int32_t pos0, int32_t seq_len,
                       int32_t n_kv_heads, int32_t head_dim, void *stream);
 
-/* Workspace for genllm_paged_decode: fp32 partial (m, l, o) per split plus one
- * counter per (kv head, row chunk).  Must be zero-filled once before first use;
- * the kernel leaves its counters at zero.  Two launches sharing a workspace
- * must be ordered (same stream). */
+/* Workspace for genllm_paged_decode: fp32 partial (m, l, o) per split (at most
+ * 256 splits).  Two launches sharing a workspace must be ordered (same stream). */
 size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int32_t seq_len,
                                            int32_t head_dim, int32_t max_pages);
 
 /* The attention loop of PagedAttentionImpl (attention.cpp:148-215) for short
  * query chunks (seq_len * n_q_heads / n_kv_heads <= 16 rows per kv head):
- * split-K over pages, GQA rows packed per kv head, LSE merge of the splits in
- * the same launch.  q/out rows addressed as base + h*head_stride + s*tok_stride
+ * split-K over pages, GQA rows packed per kv head, then a log-sum-exp merge of
+ * the splits by a second kernel on the same stream.  q/out rows addressed as base + h*head_stride + s*tok_stride
  * (elements).  n_cached = total_cached; query s sits at n_cached - seq_len + s. */
 int genllm_paged_decode(const void *q, int64_t q_head_stride, int64_t q_tok_stride, void *out,
                         int64_t o_head_stride, int64_t o_tok_stride, const void *k_pool, const void *v_pool,
@@ -189,11 +187,12 @@ int genllm_paged_prefill(const void *q, int64_t q_head_stride, int64_t q_tok_str
  * benchmark (counter-based hash -> Box-Muller -> RNE bf16). */
 int genllm_fill_normal_bf16(void *dst, size_t n, uint64_t seed, uint64_t offset, void *stream);
 
-/* No counterpart in the reference: runs one v_mfma_f32_16x16x32_bf16 on
- * a[16][32], b[32][16] (bf16, device) into c[16][16] (fp32, device) through
- * the operand layouts the kernels assume; the tests compare it with a host
- * matrix product. */
-int genllm_selftest_mfma(const void *a, const void *b, float *c, void *stream);
+/* No counterpart in the reference: runs one bf16 MFMA, k = 32
+ * (v_mfma_f32_16x16x32_bf16) or k = 16 (v_mfma_f32_16x16x16_bf16), on
+ * a[16][k], b[k][16] (bf16, device) into c[16][16] (fp32, device) through the
+ * operand layouts the kernels assume; the tests compare it with a host matrix
+ * product. */
+int genllm_selftest_mfma(int32_t k, const void *a, const void *b, float *c, void *stream);
 
 #ifdef __cplusplus
 }

@@ -21,9 +21,10 @@ def dev(bits):
     return paged.to_device_bf16(bits)
 
 
-def test_mfma_operand_layout():
-    a = synth.normal_bf16(1, (16, 32))
-    b = synth.normal_bf16(2, (32, 16))
+@pytest.mark.parametrize("k", [32, 16])
+def test_mfma_operand_layout(k):
+    a = synth.normal_bf16(1, (16, k))
+    b = synth.normal_bf16(2, (k, 16))
     c = torch.zeros((16, 16), dtype=torch.float32, device="cuda")
     paged.selftest_mfma(dev(a), dev(b), c)
     torch.cuda.synchronize()

@@ -98,10 +98,6 @@ def test_decode_shapes(orc, Hq, Hkv, N):
     q = synth.normal_bf16(2000 + N, (Hq, 1, 128))
     got, ws = ctx.decode(q)
     assert_attn_close(got, ctx.oracle(q), f"Hq{Hq} Hkv{Hkv} N{N}")
-    # the split counters are back at zero after the launch
-    G = Hq // Hkv
-    units = Hkv * ((G + 3) // 4)
-    assert not ws[: units * 4].any().item()
     ctx.close()
 
 
