@@ -10,17 +10,22 @@ MALL cannot serve them; each layer's context grows by one token per visit, as
 in a real decode loop, and the algorithmic bytes are counted per step.
 
 value = whole-step algorithmic HBM bytes / step time (GB/s).  roofline = the
-dominant kernel (paged_decode_kernel) timed alone with HIP events around each
-launch on the launch stream, against 8 TB/s.  Secondary figures (same line):
-config 2 fused append GB/s, config 4 causal prefill TFLOPS, config 5 36-layer
-long-context decode.  cpu_baseline = the oracle (single thread) on a bounded
-sample of the headline workload.
+dominant kernel (paged_decode_kernel + its split merge) timed alone with HIP
+events around each launch on the launch stream, against 8 TB/s; its HBM
+traffic comes from the committed rocprofv3 --pmc summary when present.
+Secondary figures (same line): config 2 fused append GB/s, config 4 causal
+prefill TFLOPS, config 5 36-layer long-context decode.  cpu_baseline = the
+oracle (single thread) on a bounded sample of the headline workload.
+
+--only {headline,append,prefill,longctx} runs one workload alone (for
+rocprofv3 passes); the line then carries only that workload's figures.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -28,10 +33,11 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-METRIC = ("paged decode attn µs/layer + achieved HBM GB/s (Qwen3-4B, 8K ctx); prefill TFLOPS")
+METRIC = "paged decode attn µs/layer + achieved HBM GB/s (Qwen3-4B, 8K ctx); prefill TFLOPS"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 PAGE = 16
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_config3_pmc.md")
 
 
 def parse():
@@ -40,6 +46,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
+    ap.add_argument("--only", choices=["headline", "append", "prefill", "longctx", "copy"], default=None)
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -57,30 +64,42 @@ def decode_step_bytes(n_keys: int, Hq=32, Hkv=8, D=128) -> int:
 
 
 def decode_kernel_bytes(n_keys: int, Hq=32, Hkv=8, D=128) -> int:
+    """K/V of n_keys tokens + q + out + page ids."""
     return n_keys * Hkv * D * 2 * 2 + 2 * Hq * D * 2 + ((n_keys + PAGE - 1) // PAGE) * 8
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
-              "multi-GPU sharding of the path is described in DESIGN.md, not run.", file=sys.stderr)
-        sys.exit(2)
+def committed_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
 
-    import numpy as np
-    import torch
 
-    from genllm_amd import paged, synth
-    from genllm_amd._lib import call as _call
+def time_launches(torch, fn, n, warm=5):
+    """Average duration (us) of fn(i) bracketed by HIP events on the current stream."""
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record(stream)
+        fn(warm + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return 1e3 * sum(ms) / len(ms), ms
 
-    torch.cuda.set_device(0)
-    dev_name = torch.cuda.get_device_name(0)
+
+# ----------------------------------------------------------------- headline
+def headline(args, np, torch, paged, synth, call):
     Hq, Hkv, D = 32, 8, 128
     G = Hq // Hkv
     scale = 1.0 / np.sqrt(D)
-    pool_pages = 2048
-    n0 = 8192
-    L = args.layers
+    pool_pages, n0, L = 2048, 8192, args.layers
     seed = synth.config_seed(3)
     layer_bytes = 2 * pool_pages * PAGE * Hkv * D * 2 + 4 * pool_pages * 4 + 4096
     mgr = paged.PagedAttentionManager(L * layer_bytes + (1 << 20))
@@ -91,14 +110,13 @@ def main():
         mgr.append_kv_pages(l, n0)
         info = mgr.get_layer(l)
         n_el = pool_pages * PAGE * Hkv * D
-        _call("genllm_fill_normal_bf16", info.k_pool, n_el, seed + 100 + l, 0, None)
-        _call("genllm_fill_normal_bf16", info.v_pool, n_el, seed + 200 + l, 0, None)
+        call("genllm_fill_normal_bf16", info.k_pool, n_el, seed + 100 + l, 0, None)
+        call("genllm_fill_normal_bf16", info.v_pool, n_el, seed + 200 + l, 0, None)
     q = [paged.to_device_bf16(synth.normal_bf16(seed + 300 + l, (1, Hq, 1, D))) for l in range(L)]
     kn = [paged.to_device_bf16(synth.normal_bf16(seed + 400 + l, (1, Hkv, 1, D))) for l in range(L)]
     vn = [paged.to_device_bf16(synth.normal_bf16(seed + 500 + l, (1, Hkv, 1, D))) for l in range(L)]
     out = [torch.empty((1, Hq, 1, D), dtype=torch.bfloat16, device="cuda") for _ in range(L)]
     torch.cuda.synchronize()
-
     cached = [n0] * L
 
     def op_step(i):
@@ -117,10 +135,8 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     step_s = (t1 - t0) / args.steps
-    value_gbs = total_bytes / (t1 - t0) / 1e9
-    mean_keys = total_bytes / args.steps  # for the record only
 
-    # ---- dominant kernel alone: split-K decode, 8193 keys, HIP events per launch
+    # dominant kernel alone: split-K decode + merge, 8193 keys, HIP events per launch
     n_keys = n0 + 1
     ws = torch.zeros(paged.decode_workspace_bytes(Hq, Hkv, 1, D, pool_pages), dtype=torch.uint8, device="cuda")
     infos = [mgr.get_layer(l) for l in range(L)]
@@ -128,79 +144,34 @@ def main():
     qh = [t.view(Hq, 1, D) for t in q]
 
     def kernel_launch(i):
-        l = i % L
-        inf = infos[l]
-        paged.paged_decode(qh[l], o2, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, (n_keys + 15) // 16, n_keys,
-                           Hkv, scale, ws)
+        inf = infos[i % L]
+        paged.paged_decode(qh[i % L], o2, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, (n_keys + 15) // 16,
+                           n_keys, Hkv, scale, ws)
 
-    for i in range(args.warmup):
-        kernel_launch(i)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        kernel_launch(i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    k_ms = [a.elapsed_time(b) for a, b in ev]
-    k_avg_us = 1e3 * sum(k_ms) / len(k_ms)
+    k_avg_us, k_ms = time_launches(torch, kernel_launch, args.steps, warm=args.warmup)
     kbytes = decode_kernel_bytes(n_keys)
     achieved = kbytes / (k_avg_us * 1e-6) / 1e9
-
-    result = {
-        "metric": METRIC,
-        "value": round(value_gbs, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+    traffic = committed_traffic()
+    res = {
+        "value": round(total_bytes / (t1 - t0) / 1e9, 1),
         "ms_per_step": round(step_s * 1e3, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded counter-based normal bf16 K/V/q, Fisher-Yates block tables)",
+        "us_per_layer": round(step_s * 1e6, 2),
         "config": {"workload": "BASELINE config 3: Qwen3-4B-shape paged decode, batch 1, 8K context, "
                                "append 1 token then attend (op genllm_paged_attention)",
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context_start": n0 + 1,
                    "context_end": max(cached), "pool_pages": pool_pages, "rotating_layers": L},
-        "us_per_layer": round(step_s * 1e6, 2),
-        "device": dev_name,
-        "roofline": {"kernel": "paged_decode_kernel<128>", "bound": "hbm", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": kbytes, "avg_launch_us": round(k_avg_us, 3),
-                     "p10_us": round(1e3 * np.percentile(k_ms, 10), 3),
-                     "p90_us": round(1e3 * np.percentile(k_ms, 90), 3)},
+        "roofline": {"kernel": "paged_decode_kernel<128> + paged_decode_merge_kernel<128>", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": kbytes, "avg_launch_us": round(k_avg_us, 3),
+                     "p10_us": round(1e3 * float(np.percentile(k_ms, 10)), 3),
+                     "p90_us": round(1e3 * float(np.percentile(k_ms, 90)), 3)},
     }
-
-    if not args.skip_secondary:
-        result["secondary"] = secondary(paged, synth, np, torch, args)
-
-    if not args.skip_cpu:
-        result["cpu_baseline"] = cpu_baseline(mgr, paged, synth, np, args, seed)
-    mgr.close()
-    print(json.dumps(result), flush=True)
+    return res, mgr, seed
 
 
-def time_launches(torch, fn, n, warm=5):
-    for i in range(warm):
-        fn(i)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for i in range(n):
-        ev[i][0].record(stream)
-        fn(warm + i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    ms = [a.elapsed_time(b) for a, b in ev]
-    return 1e3 * sum(ms) / len(ms), ms
-
-
-def secondary(paged, synth, np, torch, args):
-    out = {}
-    # ---- config 2: fused K/V append (q/k norm -> RoPE -> scatter), 4096 tokens
+# ---------------------------------------------------------------- secondary
+def append_cfg2(np, torch, paged, synth, call):
     S, Hkv, D, pool = 4096, 8, 128, 1024
     seed = synth.config_seed(2)
     copies = 8
@@ -227,27 +198,27 @@ def secondary(paged, synth, np, torch, args):
 
     avg_us, _ = time_launches(torch, app, n_app, warm=0)
     app_bytes = 2 * S * Hkv * D * 2 * 2 + S * (D // 2) * 4 * 2 + D * 4 + (S // PAGE) * 8
-    out["append_config2"] = {"avg_launch_us": round(avg_us, 3), "bytes": app_bytes,
-                             "GB_s": round(app_bytes / (avg_us * 1e-6) / 1e9, 1),
-                             "frac_hbm": round(app_bytes / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                             "launches": n_app}
     m2.close()
+    gbs = app_bytes / (avg_us * 1e-6) / 1e9
+    return {"avg_launch_us": round(avg_us, 3), "bytes": app_bytes, "GB_s": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "launches": n_app,
+            "note": "events bracket the C call: page-table upload (hipMemcpyAsync) + kv_append_kernel"}
 
-    # ---- config 4: causal paged prefill, 2048 tokens, Qwen3-1.7B shape
+
+def prefill_cfg4(np, torch, paged, synth, call, iters=40):
     Hq, Hkv, D, S = 16, 8, 128, 2048
     seed = synth.config_seed(4)
     copies = 4
     m4 = paged.PagedAttentionManager(copies * (2 * 128 * PAGE * Hkv * D * 2 + 8 * 128 + 4096) + (1 << 20))
     qs = []
-    from genllm_amd._lib import call as _call
     for c in range(copies):
         m4.init_layer(c, Hkv, D)
         m4.reserve_layer(c, 128)
         m4.fragment(c, synth.shuffled(seed + 2 * c, 128), synth.shuffled(seed + 2 * c + 1, 128))
         m4.append_kv_pages(c, S)
         inf = m4.get_layer(c)
-        _call("genllm_fill_normal_bf16", inf.k_pool, 128 * PAGE * Hkv * D, seed + 30 + c, 0, None)
-        _call("genllm_fill_normal_bf16", inf.v_pool, 128 * PAGE * Hkv * D, seed + 40 + c, 0, None)
+        call("genllm_fill_normal_bf16", inf.k_pool, 128 * PAGE * Hkv * D, seed + 30 + c, 0, None)
+        call("genllm_fill_normal_bf16", inf.v_pool, 128 * PAGE * Hkv * D, seed + 40 + c, 0, None)
         qq = torch.empty((S, Hq, D), dtype=torch.bfloat16, device="cuda")
         paged.fill_normal_bf16(qq, seed + 50 + c)
         qs.append(qq)
@@ -255,19 +226,19 @@ def secondary(paged, synth, np, torch, args):
     infos = [m4.get_layer(c) for c in range(copies)]
 
     def pre(i):
-        c = i % copies
-        inf = infos[c]
-        paged.paged_prefill(qs[c], o4, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, 128, S, Hkv, 1.0 / np.sqrt(D),
-                            q_layout="token")
+        inf = infos[i % copies]
+        paged.paged_prefill(qs[i % copies], o4, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, 128, S, Hkv,
+                            1.0 / np.sqrt(D), q_layout="token")
 
-    avg_us, _ = time_launches(torch, pre, 40)
+    avg_us, _ = time_launches(torch, pre, iters)
+    m4.close()
     flops = 4 * D * Hq * S * (S + 1) // 2
     tfl = flops / (avg_us * 1e-6) / 1e12
-    out["prefill_config4"] = {"avg_launch_us": round(avg_us, 3), "flops": flops, "TFLOPS": round(tfl, 1),
-                              "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}
-    m4.close()
+    return {"avg_launch_us": round(avg_us, 3), "flops": flops, "TFLOPS": round(tfl, 1),
+            "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}
 
-    # ---- config 5: 36 layers back-to-back, 32761 cached tokens each
+
+def longctx_cfg5(np, torch, paged, synth, call, iters=10):
     Hq, Hkv, D, N, pool, layers = 32, 8, 128, 32761, 4096, 36
     seed = synth.config_seed(5)
     m5 = paged.PagedAttentionManager(layers * (2 * pool * PAGE * Hkv * D * 2 + 8 * pool + 4096) + (1 << 20))
@@ -277,8 +248,8 @@ def secondary(paged, synth, np, torch, args):
         m5.fragment(l, synth.shuffled(seed + 2 * l, pool), synth.shuffled(seed + 2 * l + 1, pool))
         m5.append_kv_pages(l, N)
         inf = m5.get_layer(l)
-        _call("genllm_fill_normal_bf16", inf.k_pool, pool * PAGE * Hkv * D, seed + 100 + l, 0, None)
-        _call("genllm_fill_normal_bf16", inf.v_pool, pool * PAGE * Hkv * D, seed + 200 + l, 0, None)
+        call("genllm_fill_normal_bf16", inf.k_pool, pool * PAGE * Hkv * D, seed + 100 + l, 0, None)
+        call("genllm_fill_normal_bf16", inf.v_pool, pool * PAGE * Hkv * D, seed + 200 + l, 0, None)
     q5 = torch.empty((layers, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
     paged.fill_normal_bf16(q5, seed)
     o5 = torch.empty((Hq, 1, D), dtype=torch.bfloat16, device="cuda")
@@ -292,16 +263,27 @@ def secondary(paged, synth, np, torch, args):
             paged.paged_decode(q5[l], o5, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, n_pages, N, Hkv,
                                1.0 / np.sqrt(D), ws)
 
-    avg_us, _ = time_launches(torch, all_layers, 10, warm=2)
-    b5 = layers * decode_kernel_bytes(N)
-    out["longctx_config5"] = {"total_us": round(avg_us, 2), "us_per_layer": round(avg_us / layers, 3),
-                              "bytes": b5, "GB_s": round(b5 / (avg_us * 1e-6) / 1e9, 1),
-                              "frac_hbm": round(b5 / (avg_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    avg_us, _ = time_launches(torch, all_layers, iters, warm=2)
     m5.close()
-    return out
+    b5 = layers * decode_kernel_bytes(N)
+    gbs = b5 / (avg_us * 1e-6) / 1e9
+    return {"total_us": round(avg_us, 2), "us_per_layer": round(avg_us / layers, 3), "bytes": b5,
+            "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def cpu_baseline(mgr, paged, synth, np, args, seed):
+def copy_calibration(np, torch, paged, synth, call, mib=256, iters=20):
+    """A plain device copy of known size (torch copy_), the reference point that
+    scales the FETCH_SIZE / WRITE_SIZE counters of the rocprofv3 --pmc passes."""
+    src = torch.empty(mib << 19, dtype=torch.bfloat16, device="cuda")
+    paged.fill_normal_bf16(src, 1)
+    dst = torch.empty_like(src)
+    avg_us, _ = time_launches(torch, lambda i: dst.copy_(src), iters, warm=3)
+    nbytes = src.numel() * 2
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_launch_us": round(avg_us, 3),
+            "GB_s_read_plus_write": round(2 * nbytes / (avg_us * 1e-6) / 1e9, 1)}
+
+
+def cpu_baseline(mgr, np, paged, synth, args, seed):
     """The oracle (oracle/, single thread) on the headline step, on inputs
     copied back from layer 0 of the GPU run: same pools, same allocator state,
     same q / k / v."""
@@ -344,6 +326,55 @@ def cpu_baseline(mgr, paged, synth, np, args, seed):
                       f"Qwen3-4B shape) of the oracle restatement, gcc -O3 -mavx2 -mfma -mf16c, 1 thread",
             "us_per_step_median": round(1e6 * statistics.median(times), 1),
             "host_cores": os.cpu_count(), "cpu_model": cpu_model}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
+              "multi-GPU sharding of the path is described in DESIGN.md, not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from genllm_amd import paged, synth
+    from genllm_amd._lib import call
+
+    torch.cuda.set_device(0)
+    common = (np, torch, paged, synth, call)
+    if args.only and args.only != "headline":
+        fn = {"append": append_cfg2, "prefill": prefill_cfg4, "longctx": longctx_cfg5,
+              "copy": copy_calibration}[args.only]
+        print(json.dumps({"only": args.only, **fn(*common)}), flush=True)
+        return
+
+    head, mgr, seed = headline(args, *common)
+    result = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded counter-based normal bf16 K/V/q, Fisher-Yates block tables)",
+        "config": head["config"],
+        "us_per_layer": head["us_per_layer"],
+        "device": torch.cuda.get_device_name(0),
+        "roofline": head["roofline"],
+    }
+    if not args.skip_secondary and not args.only:
+        result["secondary"] = {"append_config2": append_cfg2(*common), "prefill_config4": prefill_cfg4(*common),
+                               "longctx_config5": longctx_cfg5(*common)}
+    if not args.skip_cpu and not args.only:
+        result["cpu_baseline"] = cpu_baseline(mgr, np, paged, synth, args, seed)
+    mgr.close()
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

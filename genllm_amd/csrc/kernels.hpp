@@ -63,6 +63,19 @@ struct AttnParams {
     // split-K decode: per-split partials [unit][split][row][D] then {m, l} per (unit, split, row)
     float* partial = nullptr;
     int32_t pages_per_split = 0, n_splits = 1, n_chunks = 1;
+    // fused append (decode of the op): tokens at positions >= new_from are read
+    // from k_new / v_new ([Hkv][S][D], strides in elements) instead of the
+    // pools and written into the pools by the wave that reads their page; page
+    // ids opened by this call come in `upd` and are written to the tables.
+    const uint16_t* k_new = nullptr;
+    const uint16_t* v_new = nullptr;
+    int64_t new_head_stride = 0, new_tok_stride = 0;
+    int32_t new_from = INT32_MAX;
+    uint16_t* k_pool_w = nullptr;  // writable aliases of k_pool / v_pool
+    uint16_t* v_pool_w = nullptr;
+    int32_t* k_ids_w = nullptr;
+    int32_t* v_ids_w = nullptr;
+    TableUpdate upd;
 };
 
 // Workspace layout of the split-K decode.

@@ -206,6 +206,10 @@ int check_attn_args(const AttnParams& p, int head_dim) {
         return fail(GENLLM_ERR_INVALID, "paged attention: n_q_heads must be a multiple of n_kv_heads");
     if (p.S <= 0 || p.n_cached < p.S || p.n_pages < (p.n_cached + kPage - 1) / kPage)
         return fail(GENLLM_ERR_INVALID, "paged attention: need 0 < seq_len <= n_cached <= 16 * n_pages");
+    // OpFactory::Attention replaces a negative scale by 1/sqrt(head_dim) (op_factory.hpp:467),
+    // so the op never sees one; the kernels rely on scale >= 0.
+    if (!(p.scale_log2 >= 0.0f) || p.scale_log2 == INFINITY)
+        return fail(GENLLM_ERR_INVALID, "paged attention: scale must be finite and >= 0");
     if (!aligned(p.q, 16) || !aligned(p.k_pool, 16) || !aligned(p.v_pool, 16) || !aligned(p.out, 8) ||
         (p.q_head_stride % 8) || (p.q_tok_stride % 8) || (p.o_head_stride % 4) || (p.o_tok_stride % 4))
         return fail(GENLLM_ERR_INVALID, "paged attention: q/pools must be 16-byte aligned, strides multiples of 8");
@@ -431,8 +435,12 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
         return fail(GENLLM_ERR_INVALID, "paged_attention: k/v must be 16-byte aligned");
     hipStream_t st = as_stream(stream);
 
-    // 1. append (append_kv_from_tensor, attention.cpp:146): head-major [Hkv][S][D]
+    // 1. append (append_kv_from_tensor, attention.cpp:146): head-major [Hkv][S][D].
+    // Short chunks (the decode kernel's range) append inside the attention
+    // kernel itself: the wave that reads a page takes the new rows from k/v and
+    // writes them to their slots, so no separate launch is needed.
     const int32_t pos0 = s->num_cached;
+    const bool fuse = int64_t(n_kv_groups) * seq_len <= 16;
     AppendParams ap;
     if (int rc = append_pages(*s, seq_len, st, &ap.upd)) return rc;
     ap.k = static_cast<const uint16_t*>(k);
@@ -448,7 +456,8 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     ap.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
     ap.k_ids = s->d_k_ids;
     ap.v_ids = s->d_v_ids;
-    if (int rc = launch_kv_append(ap, head_dim, st)) return rc;
+    if (!fuse)
+        if (int rc = launch_kv_append(ap, head_dim, st)) return rc;
     if (s->k_ids.empty()) return GENLLM_OK;  // attention.cpp:148
 
     // 2. attend over all cached tokens
@@ -473,6 +482,18 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     p.causal = causal != 0;
     p.page_elems = ap.page_elems;
     p.kv_row = int64_t(n_kv_heads) * head_dim;
+    if (fuse) {
+        p.k_new = ap.k;
+        p.v_new = ap.v;
+        p.new_head_stride = ap.k_head_stride;
+        p.new_tok_stride = ap.k_tok_stride;
+        p.new_from = pos0;
+        p.k_pool_w = s->k_base;
+        p.v_pool_w = s->v_base;
+        p.k_ids_w = s->d_k_ids;
+        p.v_ids_w = s->d_v_ids;
+        p.upd = ap.upd;
+    }
     return run_attention(p, head_dim, s->max_blocks, st, kv);
 }
 

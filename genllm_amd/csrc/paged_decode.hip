@@ -99,24 +99,71 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
     const int begin = sp * p.pages_per_split;
     const int end = min(begin + p.pages_per_split, p.n_pages);
     const int np = end - begin - wv > 0 ? (end - begin - wv + kWaves - 1) / kWaves : 0;
+    // fused append: page ids opened by this call come from the launch arguments
+    if (sp == 0 && h == 0 && threadIdx.x < p.upd.count) {
+        p.k_ids_w[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
+        p.v_ids_w[p.upd.first + threadIdx.x] = p.upd.v[threadIdx.x];
+    }
     int my_kid = 0, my_vid = 0;  // block-table entries of the wave's pages, one per lane
     if (lane < np) {
-        my_kid = p.k_ids[begin + wv + kWaves * lane];
-        my_vid = p.v_ids[begin + wv + kWaves * lane];
+        const int pg = begin + wv + kWaves * lane;
+        const int rel = pg - p.upd.first;
+        if (rel >= 0 && rel < p.upd.count) {
+            my_kid = p.upd.k[rel];
+            my_vid = p.upd.v[rel];
+        } else {
+            my_kid = p.k_ids[pg];
+            my_vid = p.v_ids[pg];
+        }
     }
-    const uint16_t* kcol = p.k_pool + h * D + n16 * p.kv_row + 8 * g;
-    const uint16_t* vcol = p.v_pool + h * D + (4 * g) * p.kv_row + 8 * n16;
+    const int64_t kcol = h * D + n16 * p.kv_row + 8 * g;        // element offsets inside a page
+    const int64_t vcol = h * D + (4 * g) * p.kv_row + 8 * n16;
+    const bool fused = p.k_new != nullptr;
     uint16_t* vt = lds_vt[wv];
 
+    // Token t >= new_from is this call's append: read it from k_new / v_new.
     auto load_page = [&](int j, PageRegs& pr) {
+        const int pg = begin + wv + kWaves * j;
         const int64_t kid = __builtin_amdgcn_readlane(my_kid, j);
         const int64_t vid = __builtin_amdgcn_readlane(my_vid, j);
-        const uint16_t* kb = kcol + kid * p.page_elems;
-        const uint16_t* vb = vcol + vid * p.page_elems;
+        const uint16_t* kb = p.k_pool + kid * p.page_elems + kcol;
+        const uint16_t* vb = p.v_pool + vid * p.page_elems + vcol;
+        if (fused) {
+            const int tk = pg * kPage + n16;
+            if (tk >= p.new_from && tk < p.n_cached)
+                kb = p.k_new + h * p.new_head_stride + int64_t(tk - p.new_from) * p.new_tok_stride + 8 * g;
+        }
 #pragma unroll
         for (int c = 0; c < KS; ++c) pr.k[c] = *reinterpret_cast<const uint4*>(kb + 32 * c);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pr.v[i] = *reinterpret_cast<const uint4*>(vb + i * p.kv_row);
+        for (int i = 0; i < 4; ++i) {
+            const uint16_t* src = vb + i * p.kv_row;
+            if (fused) {
+                const int tv = pg * kPage + 4 * g + i;
+                if (tv >= p.new_from && tv < p.n_cached)
+                    src = p.v_new + h * p.new_head_stride + int64_t(tv - p.new_from) * p.new_tok_stride + 8 * n16;
+            }
+            pr.v[i] = *reinterpret_cast<const uint4*>(src);
+        }
+    };
+    // ... and write the appended rows into their page slots (bit-exact copies)
+    auto store_new = [&](int j, const PageRegs& pr) {
+        const int pg = begin + wv + kWaves * j;
+        if (pg * kPage + kPage <= p.new_from) return;  // wave-uniform: no new token in this page
+        const int64_t kid = __builtin_amdgcn_readlane(my_kid, j);
+        const int64_t vid = __builtin_amdgcn_readlane(my_vid, j);
+        const int tk = pg * kPage + n16;
+        if (tk >= p.new_from && tk < p.n_cached) {
+            uint16_t* dst = p.k_pool_w + kid * p.page_elems + kcol;
+#pragma unroll
+            for (int c = 0; c < KS; ++c) *reinterpret_cast<uint4*>(dst + 32 * c) = pr.k[c];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tv = pg * kPage + 4 * g + i;
+            if (tv >= p.new_from && tv < p.n_cached)
+                *reinterpret_cast<uint4*>(p.v_pool_w + vid * p.page_elems + vcol + i * p.kv_row) = pr.v[i];
+        }
     };
 
     float m_run = -INFINITY, l_run = 0.0f;
@@ -200,6 +247,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
             const int j = j0 + u;
             if (j < np) {
                 if (j + PF - 1 < np) load_page(j + PF - 1, buf[(u + PF - 1) % PF]);
+                if (fused) store_new(j, buf[u]);
                 compute_page(j, buf[u]);
             }
         }
@@ -251,55 +299,75 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
 }
 
 // Merge of the splits: one workgroup per (row, kv head).  Wave w takes splits
-// w, w+4, ...; lane -> 2 dims; the waves' sums meet in LDS.
+// w, w+4, ... (lane -> 2 dims) and issues the loads of up to 16 of them before
+// reducing the (m, l) of all splits, so the merge costs about one memory round
+// trip; the waves' sums meet in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
-    __shared__ float w_tab[kMaxSplits];
-    __shared__ float part[kWaves][D + 2];
+    constexpr int B = 16;  // o partials in flight per lane
+    __shared__ float part[kWaves][D];
+    __shared__ float s_L;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ri = blockIdx.x, h = blockIdx.y;
     const int rows = p.G * p.S;
-    const int ns = p.n_splits;
+    const int ns = p.n_splits;  // <= kMaxSplits = 256
+    const int d2 = lane * 2;
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
                        int64_t(h) * ns * rows + ri;
-    // max over splits, then (wave 0) weights 2^(m_s - M) and L
-    float mx = -INFINITY;
-    for (int s2 = lane; s2 < ns; s2 += 64) mx = fmaxf(mx, ml[s2 * rows].x);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (wv == 0) {
-        float lsum = 0.0f;
-        for (int s2 = lane; s2 < ns; s2 += 64) {
-            const float2 v = ml[s2 * rows];
-            const float e = (mx == -INFINITY || v.x == -INFINITY) ? 0.0f : exp2_fast(v.x - mx);
-            w_tab[s2] = e;
-            lsum += v.y * e;
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
-        if (lane == 0) part[0][D] = lsum;
-    }
-    __syncthreads();
-    const int d2 = lane * 2;
     const float2* po = reinterpret_cast<const float2*>(p.partial + (int64_t(h) * ns * rows + ri) * D + d2);
     const int64_t sstride = int64_t(rows) * D / 2;  // float2 units between splits
+
+    float2 ov[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        const int s2 = wv + kWaves * u;
+        ov[u] = s2 < ns ? po[s2 * sstride] : make_float2(0.0f, 0.0f);
+    }
+    float2 mlv[kMaxSplits / 64];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / 64; ++k) {
+        const int s2 = lane + 64 * k;
+        mlv[k] = s2 < ns ? ml[s2 * rows] : make_float2(-INFINITY, 0.0f);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / 64; ++k) mx = fmaxf(mx, mlv[k].x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    auto weight = [&](float m) { return (mx == -INFINITY || m == -INFINITY) ? 0.0f : exp2_fast(m - mx); };
+    if (wv == 0) {
+        float lsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kMaxSplits / 64; ++k) lsum += mlv[k].y * weight(mlv[k].x);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+        if (lane == 0) s_L = lsum;
+    }
+    // m of split s2 lives in lane s2 % 64, slot s2 / 64
+    auto m_of = [&](int s2) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kMaxSplits / 64; ++k) {
+            const float v = __shfl(mlv[k].x, s2 & 63);
+            if ((s2 >> 6) == k) m = v;
+        }
+        return m;
+    };
     float a0 = 0.0f, a1 = 0.0f;
-    int s2 = wv;
-    for (; s2 + 3 * kWaves < ns; s2 += 4 * kWaves) {  // 4 independent loads per lane per step
-        float2 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = po[(s2 + u * kWaves) * sstride];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float wgt = w_tab[s2 + u * kWaves];
-            a0 += v[u].x * wgt;
-            a1 += v[u].y * wgt;
+    for (int u = 0; u < B; ++u) {
+        const int s2 = wv + kWaves * u;
+        if (s2 < ns) {
+            const float w = weight(m_of(s2));
+            a0 += ov[u].x * w;
+            a1 += ov[u].y * w;
         }
     }
-    for (; s2 < ns; s2 += kWaves) {
+    for (int s2 = wv + kWaves * B; s2 < ns; s2 += kWaves) {  // more than 64 splits
         const float2 v = po[s2 * sstride];
-        a0 += v.x * w_tab[s2];
-        a1 += v.y * w_tab[s2];
+        const float w = weight(m_of(s2));
+        a0 += v.x * w;
+        a1 += v.y * w;
     }
     part[wv][d2] = a0;
     part[wv][d2 + 1] = a1;
@@ -311,7 +379,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
             o0 += part[w2][d2];
             o1 += part[w2][d2 + 1];
         }
-        const float inv = 1.0f / part[0][D];
+        const float inv = 1.0f / s_L;
         uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
         *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(o0 * inv), f32_to_bf16_ref(o1 * inv));
     }

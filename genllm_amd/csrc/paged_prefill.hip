@@ -103,6 +103,10 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     static_assert(KCH * NT == KT * (D / 8) && VTK * NT == (KT / 2) * (D / 8), "tile split");
     static_assert(NT % (KT / 2) == 0 && (NT / (D / 8)) * KCH == KT && KCH == KT / kPage, "thread map");
     uint4 kreg[KCH], va[VTK], vb[VTK];
+    // in-page element offsets are the same for every tile (tiles start on page boundaries)
+    const int tp = tid & (KT / 2 - 1);
+    const uint16_t* kbase = p.k_pool + (tid >> 4) * p.kv_row + hkv * D + 8 * (tid & 15);
+    const uint16_t* vbase = p.v_pool + ((2 * tp) % kPage) * p.kv_row + hkv * D + 8 * (tid >> 5);
     auto load_ids = [&](int tile) -> int {
         const int page = 4 * tile + (lane & 3);
         int id = 0;
@@ -111,23 +115,31 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     };
     auto load_tile = [&](int tile, int ids) {
         const int tok0 = tile * KT;
+        const int64_t vid = __shfl(ids, 4 + (tp >> 3));
+        if (tok0 + KT <= p.n_cached) {  // whole tile cached: no per-load conditions
+#pragma unroll
+            for (int e = 0; e < KCH; ++e)
+                kreg[e] = *reinterpret_cast<const uint4*>(kbase + int64_t(__builtin_amdgcn_readlane(ids, e)) *
+                                                                      p.page_elems);
+#pragma unroll
+            for (int e = 0; e < VTK; ++e) {
+                const uint16_t* src = vbase + vid * p.page_elems + 8 * (NT / 32) * e;
+                va[e] = *reinterpret_cast<const uint4*>(src);
+                vb[e] = *reinterpret_cast<const uint4*>(src + p.kv_row);
+            }
+            return;
+        }
 #pragma unroll
         for (int e = 0; e < KCH; ++e) {
-            const int tt = 16 * e + (tid >> 4), ch = tid & 15;
-            const int pos = tok0 + tt;
+            const int pos = tok0 + 16 * e + (tid >> 4);
             const int64_t id = __builtin_amdgcn_readlane(ids, e);
             kreg[e] = make_uint4(0, 0, 0, 0);
-            if (pos < p.n_cached)
-                kreg[e] = *reinterpret_cast<const uint4*>(p.k_pool + id * p.page_elems +
-                                                          int64_t(pos % kPage) * p.kv_row + hkv * D + 8 * ch);
+            if (pos < p.n_cached) kreg[e] = *reinterpret_cast<const uint4*>(kbase + id * p.page_elems);
         }
-        const int tp = tid & (KT / 2 - 1);
-        const int64_t vid = __shfl(ids, 4 + (tp >> 3));
+        const int pos = tok0 + 2 * tp;
 #pragma unroll
         for (int e = 0; e < VTK; ++e) {
-            const int ch = (tid >> 5) + (NT / 32) * e;
-            const int pos = tok0 + 2 * tp;
-            const uint16_t* src = p.v_pool + vid * p.page_elems + int64_t(pos % kPage) * p.kv_row + hkv * D + 8 * ch;
+            const uint16_t* src = vbase + vid * p.page_elems + 8 * (NT / 32) * e;
             va[e] = make_uint4(0, 0, 0, 0);
             vb[e] = make_uint4(0, 0, 0, 0);
             if (pos < p.n_cached) va[e] = *reinterpret_cast<const uint4*>(src);
@@ -143,7 +155,6 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
             *reinterpret_cast<uint4*>(&kl[tt * KROW + 8 * ch]) = kreg[e];
         }
         // V transposed: the dword at V^T[d][2tp] packs tokens 2tp (low) and 2tp+1 (high)
-        const int tp = tid & (KT / 2 - 1);
 #pragma unroll
         for (int e = 0; e < VTK; ++e) {
             const int ch = (tid >> 5) + (NT / 32) * e;
@@ -153,8 +164,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
             for (int q = 0; q < 4; ++q) {
                 uint32_t* row0 = reinterpret_cast<uint32_t*>(&vl[(8 * ch + 2 * q) * VROW + 2 * tp]);
                 uint32_t* row1 = reinterpret_cast<uint32_t*>(&vl[(8 * ch + 2 * q + 1) * VROW + 2 * tp]);
-                *row0 = (av[q] & 0xFFFFu) | (bv[q] << 16);
-                *row1 = (av[q] >> 16) | (bv[q] & 0xFFFF0000u);
+                *row0 = __builtin_amdgcn_perm(bv[q], av[q], 0x05040100u);  // low halves
+                *row1 = __builtin_amdgcn_perm(bv[q], av[q], 0x07060302u);  // high halves
             }
         }
     };
@@ -196,44 +207,60 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 
         // ---- online softmax, per lane = per query row
         const bool need_mask = (p.causal && tok0 + KT - 1 > w_first_abs) || tok0 + KT > p.n_cached;
-        float alpha[2];
+        // Lazy rescale: a row's reference max m only moves (and its l, O^T are
+        // rescaled) when the tile max exceeds it by more than 2^8, so p <= 256.
+        // max over raw scores (scale >= 0), then p = exp2(s * scale*log2e - m), one fma
+        const float c = p.scale_log2;
+        float mx[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const int qpos = qabs0 + q0 + 16 * nb + n16;
-            float mx = -INFINITY;
+            float mr = -INFINITY;
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = s[mb][nb][i] * p.scale_log2;
                     if (need_mask) {
                         const int kpos = tok0 + 16 * mb + 4 * g + i;
-                        if (kpos >= p.n_cached || (p.causal && kpos > qpos)) v = -INFINITY;
+                        if (kpos >= p.n_cached || (p.causal && kpos > qpos)) s[mb][nb][i] = -INFINITY;
                     }
-                    s[mb][nb][i] = v;
-                    mx = fmaxf(mx, v);
+                    mr = fmaxf(mr, s[mb][nb][i]);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m[nb], mx);
-            const float mu = mn == -INFINITY ? 0.0f : mn;
-            alpha[nb] = exp2_fast(m[nb] - mu);
+            mr = fmaxf(mr, __shfl_xor(mr, 16));
+            mr = fmaxf(mr, __shfl_xor(mr, 32));
+            mx[nb] = mr == -INFINITY ? -INFINITY : mr * c;
+        }
+        const bool grow0 = mx[0] > m[0] + 8.0f, grow1 = mx[1] > m[1] + 8.0f;
+        if (__any(grow0 || grow1)) {
+            float alpha[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const bool grow = nb ? grow1 : grow0;
+                const float mn = grow ? mx[nb] : m[nb];
+                alpha[nb] = grow ? exp2_fast(m[nb] - mn) : 1.0f;
+                l[nb] *= alpha[nb];
+                m[nb] = mn;
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) acc[db][nb] *= alpha[nb];
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const float mu = m[nb] == -INFINITY ? 0.0f : m[nb];
             float sum = 0.0f;
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float e = exp2_fast(s[mb][nb][i] - mu);
+                    float e = exp2_fast(__builtin_fmaf(s[mb][nb][i], c, -mu));
+                    if (need_mask && s[mb][nb][i] == -INFINITY) e = 0.0f;  // also when scale == 0
                     s[mb][nb][i] = e;
                     sum += e;
                 }
-            l[nb] = l[nb] * alpha[nb] + sum;
-            m[nb] = mn;
+            l[nb] += sum;
         }
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) acc[db][nb] *= alpha[nb];
 
         // ---- O^T += V^T P^T
 #pragma unroll
