@@ -60,6 +60,11 @@ struct AttnParams {
     int32_t causal = 1;
     int64_t page_elems = 0;
     int64_t kv_row = 0;       // elements between consecutive tokens in a page (Hkv * D)
+    // Elements between kv heads (0 = head_dim, the page layout [16][Hkv][D]).
+    // With k_ids == v_ids == nullptr page i is block i: a contiguous head-major
+    // [Hkv][S][D] tensor is then kv_head_stride = S*D, kv_row = D,
+    // page_elems = 16*D (non-paged attention; prefill kernel only).
+    int64_t kv_head_stride = 0;
     // split-K decode: per-split partials [unit][split][row][D] then {m, l} per (unit, split, row)
     float* partial = nullptr;
     int32_t pages_per_split = 0, n_splits = 1, n_chunks = 1;

@@ -682,3 +682,46 @@ extern "C" int genllm_paged_prefill(const void* q, int64_t q_head_stride, int64_
     if (int rc = check_attn_args(p, head_dim)) return rc;
     return launch_paged_prefill(p, head_dim, as_stream(stream));
 }
+
+// Non-paged attention (FlashAttentionImpl, attention.cpp:39-121): the prefill
+// kernel reading K/V straight from the [B][Hkv][S][D] tensors -- page i of a
+// head is rows 16i..16i+15 of that head, so no block table is involved.  Query
+// s attends keys 0..s (causal) or all S keys; one launch per batch entry.
+extern "C" int genllm_flash_attention(const void* q, const void* k, const void* v, void* out, int32_t batch,
+                                      int32_t n_q_heads, int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
+                                      int32_t n_kv_groups, float scale, int32_t causal, void* stream) {
+    if (!q || !k || !v || !out) return fail(GENLLM_ERR_INVALID, "flash_attention: null tensor");
+    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "flash_attention requires head_dim == 128");
+    if (batch < 0 || seq_len < 0 || n_kv_heads <= 0 || n_kv_groups <= 0 || n_q_heads != n_kv_heads * n_kv_groups)
+        return fail(GENLLM_ERR_INVALID, "flash_attention: n_q_heads must equal n_kv_heads * n_kv_groups");
+    if (!(scale >= 0.0f) || scale == INFINITY)
+        return fail(GENLLM_ERR_INVALID, "flash_attention: scale must be finite and >= 0");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 8))
+        return fail(GENLLM_ERR_INVALID, "flash_attention: tensors must be 16-byte aligned");
+    const int64_t D = head_dim, S = seq_len;
+    for (int32_t b = 0; b < batch && seq_len > 0; ++b) {
+        AttnParams p;
+        p.q = static_cast<const uint16_t*>(q) + int64_t(b) * n_q_heads * S * D;
+        p.q_head_stride = S * D;
+        p.q_tok_stride = D;
+        p.out = static_cast<uint16_t*>(out) + int64_t(b) * n_q_heads * S * D;
+        p.o_head_stride = S * D;
+        p.o_tok_stride = D;
+        p.k_pool = static_cast<const uint16_t*>(k) + int64_t(b) * n_kv_heads * S * D;
+        p.v_pool = static_cast<const uint16_t*>(v) + int64_t(b) * n_kv_heads * S * D;
+        p.k_ids = p.v_ids = nullptr;
+        p.n_pages = int32_t((S + kPage - 1) / kPage);
+        p.n_cached = seq_len;
+        p.S = seq_len;
+        p.Hq = n_q_heads;
+        p.Hkv = n_kv_heads;
+        p.G = n_kv_groups;
+        p.scale_log2 = scale * kLog2e;
+        p.causal = causal != 0;
+        p.page_elems = kPage * D;
+        p.kv_row = D;
+        p.kv_head_stride = S * D;
+        if (int rc = launch_paged_prefill(p, head_dim, as_stream(stream))) return rc;
+    }
+    return GENLLM_OK;
+}

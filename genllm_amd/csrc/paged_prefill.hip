@@ -105,12 +105,14 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     uint4 kreg[KCH], va[VTK], vb[VTK];
     // in-page element offsets are the same for every tile (tiles start on page boundaries)
     const int tp = tid & (KT / 2 - 1);
-    const uint16_t* kbase = p.k_pool + (tid >> 4) * p.kv_row + hkv * D + 8 * (tid & 15);
-    const uint16_t* vbase = p.v_pool + ((2 * tp) % kPage) * p.kv_row + hkv * D + 8 * (tid >> 5);
+    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
+    const uint16_t* kbase = p.k_pool + (tid >> 4) * p.kv_row + head_off + 8 * (tid & 15);
+    const uint16_t* vbase = p.v_pool + ((2 * tp) % kPage) * p.kv_row + head_off + 8 * (tid >> 5);
+    const bool paged = p.k_ids != nullptr;
     auto load_ids = [&](int tile) -> int {
         const int page = 4 * tile + (lane & 3);
         int id = 0;
-        if (lane < 8 && page * kPage < kv_end) id = lane < 4 ? p.k_ids[page] : p.v_ids[page];
+        if (lane < 8 && page * kPage < kv_end) id = !paged ? page : lane < 4 ? p.k_ids[page] : p.v_ids[page];
         return id;
     };
     auto load_tile = [&](int tile, int ids) {

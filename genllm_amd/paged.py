@@ -282,6 +282,18 @@ def paged_prefill(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: 
          _stream(stream))
 
 
+def flash_attention(q, k, v, out, n_kv_groups: int, scale: float, causal: bool = True, stream=None):
+    """FlashAttentionImpl (attention.cpp:39-121) on contiguous bf16 tensors:
+    q, out [B, Hq, S, D]; k, v [B, Hkv, S, D]; no KV cache involved."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    for t, shape in ((q, (B, Hq, S, D)), (out, (B, Hq, S, D)), (k, (B, Hkv, S, D)), (v, (B, Hkv, S, D))):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise ValueError(f"flash_attention: expected contiguous bf16 {shape}, got {tuple(t.shape)} {t.dtype}")
+    call("genllm_flash_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, Hq, S, Hkv, D, n_kv_groups,
+         float(scale), int(causal), _stream(stream))
+
+
 def fill_normal_bf16(t: torch.Tensor, seed: int, offset: int = 0, stream=None):
     call("genllm_fill_normal_bf16", _ptr(t), t.numel(), seed, offset, _stream(stream))
 
@@ -303,6 +315,6 @@ def to_host_bits(t: torch.Tensor) -> np.ndarray:
 
 __all__ = [
     "PagedAttentionManager", "paged_attention", "qk_norm_rope_append", "rms_norm", "apply_rope", "rope_cache",
-    "kv_scatter", "paged_decode", "paged_prefill", "decode_workspace_bytes", "fill_normal_bf16",
+    "kv_scatter", "paged_decode", "paged_prefill", "flash_attention", "decode_workspace_bytes", "fill_normal_bf16",
     "selftest_mfma", "device_view", "to_device_bf16", "to_host_bits", "GenllmError", "PAGE", "DTYPE_BF16",
 ]

@@ -182,6 +182,16 @@ int genllm_paged_prefill(const void *q, int64_t q_head_stride, int64_t q_tok_str
                          int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
                          int32_t causal, void *stream);
 
+/* FlashAttentionImpl<D>::execute (src/backend/cpu/attention.cpp:39-121,
+ * src/backend/cuda/attention.cu:226-399): attention over the node's own K/V,
+ * no cache (the op type of kv_cache_per_layer = 0, README.md:97).  q, out:
+ * [batch][n_q_heads][seq_len][head_dim]; k, v: [batch][n_kv_heads][seq_len][head_dim],
+ * contiguous bf16.  kv head = q head / n_kv_groups; causal masks key s_kv > s_q.
+ * head_dim != 128 returns GENLLM_ERR_UNSUPPORTED. */
+int genllm_flash_attention(const void *q, const void *k, const void *v, void *out, int32_t batch,
+                           int32_t n_q_heads, int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
+                           int32_t n_kv_groups, float scale, int32_t causal, void *stream);
+
 /* ------------------------------------------------------------ utilities
  * No counterpart in the reference: synthetic seeded inputs for tests and the
  * benchmark (counter-based hash -> Box-Muller -> RNE bf16). */

@@ -1,0 +1,398 @@
+// test_ops_hip.cpp -- the HIP backend driven through the reference's operator
+// interface (Tensor nodes -> kernel::dispatch -> ops::*Impl<Device::HIP>), in
+// the style of the reference's tests/test_page_attention.cpp and
+// tests/test_ops_cpu.cpp.  Results are checked against the CPU restatement in
+// oracle/ (liboracle.so): page tables and K/V pages bit-exact, RMSNorm /
+// RoPE / rope tables bit-exact, attention within max-abs <= 2^-7 * max|ref|
+// and relative L2 <= 1e-2.  Needs one GPU.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#include "genllm/kernels.hpp"
+#include "genllm/manager.hpp"
+#include "genllm/page_attention.hpp"
+#include "genllm/tensor.hpp"
+#include "genllm_paged.h"
+#include "oracle.h"
+#include "test_utils.hpp"
+
+namespace {
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    explicit DevBuf(size_t n) : bytes(n) {
+        if (hipMalloc(&p, n ? n : 16) != hipSuccess) throw std::runtime_error("hipMalloc failed");
+    }
+    ~DevBuf() { (void)hipFree(p); }
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+};
+
+template <typename T>
+std::vector<T> to_host(const void* dev, size_t n) {
+    std::vector<T> h(n);
+    if (hipDeviceSynchronize() != hipSuccess || hipMemcpy(h.data(), dev, n * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+        throw std::runtime_error("device -> host copy failed");
+    return h;
+}
+
+template <typename T>
+void to_device(void* dev, const std::vector<T>& h) {
+    if (hipMemcpy(dev, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+        throw std::runtime_error("host -> device copy failed");
+}
+
+// seeded N(0,1) bf16 on the device (libgenllm_hip's generator), plus a host copy
+std::vector<uint16_t> fill_normal(DevBuf& b, uint64_t seed) {
+    const size_t n = b.bytes / 2;
+    if (genllm_fill_normal_bf16(b.p, n, seed, 0, nullptr) != GENLLM_OK) throw std::runtime_error(genllm_last_error());
+    return to_host<uint16_t>(b.p, n);
+}
+
+Tensor make_tensor(void* data, std::array<int64_t, 4> dims, DataType dt = DataType::GGML_TYPE_BF16) {
+    Tensor t;
+    t.data = data;
+    t.device = Device::HIP;
+    t.dtype = dt;
+    t.dims = dims;
+    return t;
+}
+
+// max-abs <= 2^-7 * max|ref| and rel-L2 <= 1e-2 (bf16 output, fp32 accumulation)
+bool attn_close(const std::vector<uint16_t>& got, const std::vector<uint16_t>& want, const char* what) {
+    if (got.size() != want.size()) return false;
+    double max_ref = 0, max_err = 0, num = 0, den = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        const double a = or_bf16_to_f32(got[i]), b = or_bf16_to_f32(want[i]);
+        if (!std::isfinite(a)) {
+            std::printf("    %s: non-finite output at %zu\n", what, i);
+            return false;
+        }
+        max_ref = std::max(max_ref, std::abs(b));
+        max_err = std::max(max_err, std::abs(a - b));
+        num += (a - b) * (a - b);
+        den += b * b;
+    }
+    const double rel = den > 0 ? std::sqrt(num / den) : std::sqrt(num);
+    const bool ok = max_err <= max_ref / 128.0 && rel <= 1e-2;
+    std::printf("    %s: max_abs %.3g (bound %.3g) rel_l2 %.3g\n", what, max_err, max_ref / 128.0, rel);
+    return ok;
+}
+
+// ---------------------------------------------------------------- enums
+bool test_device_enum() {
+    // tests/test_tensor.cpp:72-76, plus the HIP value
+    ASSERT(static_cast<int>(Device::CPU) == 0, "cpu=0");
+    ASSERT(static_cast<int>(Device::CUDA) == 1, "cuda=1");
+    ASSERT(static_cast<int>(Device::HIP) == 2, "hip=2");
+    ASSERT(static_cast<int>(Device::VULKAN) == 4, "vulkan=4");
+    ASSERT(static_cast<int>(OperationType::OP_TYPE_PAGED_ATTN) == 24, "paged attn op id");
+    ASSERT(static_cast<int>(DataType::GGML_TYPE_BF16) == 30, "bf16 id");
+    return true;
+}
+
+// ---------------------------------------------- tests/test_page_attention.cpp
+bool test_block_pool_alloc_free() {
+    PagedAttentionManager mgr(0, 64 << 20);
+    mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
+    mgr.reserve_layer(0, 100);
+    BlockPool pool = mgr.get_layer(0).k_pool;
+    ASSERT(pool.num_blocks() == 0, "initially 0 blocks");
+    ASSERT(pool.num_free() == 0, "initially 0 free");
+    const int32_t id = pool.alloc();
+    ASSERT(id == 0, "first alloc returns 0");
+    ASSERT(pool.num_blocks() == 1, "1 block after alloc");
+    ASSERT(pool.alloc() == 1, "second alloc returns 1");
+    pool.free(id);
+    ASSERT(pool.num_free() == 1, "1 free after free");
+    ASSERT(pool.alloc() == id, "reuse freed block");
+    ASSERT(pool.num_free() == 0, "0 free after re-alloc");
+    ASSERT(pool.block_data(1) == static_cast<char*>(pool.block_data(0)) + 16 * 8 * 128 * 2, "block stride");
+    ASSERT(pool.block_data(2) == nullptr, "no data past num_blocks");
+    return true;
+}
+
+bool test_block_pool_many_allocs() {
+    PagedAttentionManager mgr(0, 8 << 20);
+    mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
+    mgr.reserve_layer(0, 10);
+    BlockPool pool = mgr.get_layer(0).v_pool;
+    for (int i = 0; i < 10; i++) ASSERT(pool.alloc() >= 0, "alloc within capacity");
+    ASSERT(pool.alloc() == -1, "beyond capacity returns -1");
+    return true;
+}
+
+bool test_block_pool_reset() {
+    PagedAttentionManager mgr(0, 8 << 20);
+    mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
+    mgr.reserve_layer(0, 10);
+    BlockPool pool = mgr.get_layer(0).k_pool;
+    (void)pool.alloc();
+    (void)pool.alloc();
+    (void)pool.alloc();
+    mgr.reset();
+    ASSERT(pool.num_blocks() == 3, "reset keeps num_blocks");
+    ASSERT(pool.num_free() == 3, "reset adds all back to free");
+    ASSERT(pool.alloc() == 2, "free list [0,1,2] pops 2");
+    return true;
+}
+
+bool test_page_table_append_kv() {
+    PagedAttentionManager mgr(0, 1 << 20);
+    mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
+    ASSERT(mgr.get_layer(0).active, "layer active");
+    ASSERT(mgr.get_layer(0).num_cached == 0, "initially 0 cached");
+    mgr.append_kv_pages(0, 1);
+    ASSERT(mgr.get_layer(0).num_cached == 1, "1 token cached");
+    mgr.append_kv_pages(0, 31);
+    ASSERT(mgr.get_layer(0).num_cached == 32, "32 tokens cached");
+    ASSERT(mgr.get_layer(0).page_table.size() == 2, "2 pages (16+16)");
+    return true;
+}
+
+bool test_page_table_multi_layer() {
+    PagedAttentionManager mgr(0, 1 << 20);
+    mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_F16);
+    mgr.init_layer(1, 4, 64, DataType::GGML_TYPE_F32);
+    ASSERT(mgr.is_active(0), "layer 0 active");
+    ASSERT(mgr.is_active(1), "layer 1 active");
+    ASSERT(!mgr.is_active(2), "layer 2 not active");
+    mgr.append_kv_pages(0, 5);
+    mgr.append_kv_pages(1, 20);
+    ASSERT(mgr.get_layer(0).num_cached == 5, "layer0 cached 5");
+    ASSERT(mgr.get_layer(1).num_cached == 20, "layer1 cached 20");
+    mgr.reset();
+    ASSERT(mgr.get_layer(0).num_cached == 0, "after reset layer0 = 0");
+    ASSERT(mgr.get_layer(1).page_table.empty(), "after reset page_table empty");
+    return true;
+}
+
+// ------------------------------------------- scheduler rules and the switch
+bool test_kv_cache_per_layer_switch() {
+    ASSERT(attention_op_type(0) == OperationType::OP_TYPE_FLASH_ATTN, "0 -> flash attention");
+    ASSERT(attention_op_type(1) == OperationType::OP_TYPE_PAGED_ATTN, "1 -> paged attention");
+    ASSERT(attention_op_type(4) == OperationType::OP_TYPE_PAGED_ATTN, ">1 -> paged attention");
+    Tensor k = make_tensor(nullptr, {1, 8, 1, 128});
+    Tensor paged = make_tensor(nullptr, {1, 32, 1, 128});
+    paged.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+    paged.src[1] = &k;
+    paged.layer_id = 0;
+    Tensor flash = paged;
+    flash.op_type = OperationType::OP_TYPE_FLASH_ATTN;
+    flash.layer_id = 1;
+    // scheduler.cpp:363-372: 2 * ceil(max_seq/16) * 16 * Hkv * D * elem
+    ASSERT(kv_cache_bytes({&paged}, Device::HIP, 300, 1.0f) == size_t(2) * 19 * 16 * 8 * 128 * 2, "paged sizing");
+    ASSERT(kv_cache_bytes({&flash}, Device::HIP, 300, 1.0f) == 0, "flash attention owns no pages");
+    ASSERT(kv_cache_bytes({&paged}, Device::CPU, 300, 1.0f) == 0, "other device not counted");
+    return true;
+}
+
+// ------------------------------------- the op through the executor's switch
+// A two-layer graph of PAGED_ATTN nodes: prefill chunk of `s0` tokens, then
+// `steps` decode tokens, every call checked against or_paged_attention.
+bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t seed) {
+    const int32_t D = 128, G = Hq / Hkv, max_seq = 256, L = 2;
+    const float scale = 1.0f / std::sqrt(float(D));
+    MemoryManager mm;
+    std::vector<Tensor> ks(L), nodes(L);
+    std::vector<Tensor*> graph;
+    for (int l = 0; l < L; ++l) {
+        ks[l] = make_tensor(nullptr, {1, Hkv, 1, D});
+        nodes[l] = make_tensor(nullptr, {1, Hq, 1, D});
+        nodes[l].op_type = OperationType::OP_TYPE_PAGED_ATTN;
+        nodes[l].src[1] = &ks[l];
+        nodes[l].layer_id = l;
+        graph.push_back(&nodes[l]);
+    }
+    const size_t bytes = kv_cache_bytes(graph, Device::HIP, max_seq) + (1 << 20);
+    PagedAttentionManager& pam = mm.create_attention_manager(Device::HIP, 0, bytes);
+    initialize_kv_cache(pam, graph, max_seq);
+
+    or_manager* ref = or_mgr_create(1);
+    for (int l = 0; l < L; ++l) {
+        or_mgr_init_layer(ref, l, Hkv, D, OR_DTYPE_BF16);
+        or_mgr_reserve_layer(ref, l, (max_seq + 15) / 16);
+    }
+    bool ok = true;
+    for (int step = 0; step <= steps && ok; ++step) {
+        const int32_t S = step == 0 ? s0 : 1;
+        for (int l = 0; l < L && ok; ++l) {
+            DevBuf q(size_t(Hq) * S * D * 2), k(size_t(Hkv) * S * D * 2), v(size_t(Hkv) * S * D * 2),
+                o(size_t(Hq) * S * D * 2);
+            const uint64_t sd = seed + 1000 * step + 10 * l;
+            auto hq = fill_normal(q, sd), hk = fill_normal(k, sd + 1), hv = fill_normal(v, sd + 2);
+            Tensor Q = make_tensor(q.p, {1, Hq, S, D}), K = make_tensor(k.p, {1, Hkv, S, D}),
+                   V = make_tensor(v.p, {1, Hkv, S, D});
+            Tensor out = make_tensor(o.p, {1, Hq, S, D});
+            out.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+            out.layer_id = l;
+            out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
+            out.op_params = {float(D), scale, 1.0f, float(G)};
+            ASSERT(kernel::dispatch(&out, 0), "executor dispatches PAGED_ATTN");
+            std::vector<uint16_t> want(size_t(Hq) * S * D);
+            or_paged_attention(ref, l, hq.data(), hk.data(), hv.data(), want.data(), 1, Hq, S, D, Hkv, G, scale, 1);
+            char what[96];
+            std::snprintf(what, sizeof what, "Hq%d Hkv%d layer %d step %d (S=%d)", Hq, Hkv, l, step, S);
+            ok = attn_close(to_host<uint16_t>(o.p, want.size()), want, what);
+            // page placement: tables and pools bit-exact
+            const auto st = pam.get_layer(l);
+            std::vector<int32_t> rk(st.page_table.size()), rv(st.page_table.size());
+            const int32_t n = or_mgr_get_page_table(ref, l, rk.data(), rv.data(), int32_t(rk.size()));
+            ASSERT(n == int32_t(st.page_table.size()), "page table length");
+            for (int32_t i = 0; i < n; ++i)
+                ASSERT(st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
+            ASSERT(st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
+        }
+    }
+    for (int l = 0; l < L && ok; ++l) {
+        const auto st = pam.get_layer(l);
+        const size_t pool_elems = size_t(st.k_pool.num_blocks()) * 16 * Hkv * D;
+        const auto dk = to_host<uint16_t>(st.k_pool.block_data(0), pool_elems);
+        const auto dv = to_host<uint16_t>(st.v_pool.block_data(0), pool_elems);
+        ASSERT(std::memcmp(dk.data(), or_mgr_k_pool(ref, l), pool_elems * 2) == 0, "K pages bit-exact");
+        ASSERT(std::memcmp(dv.data(), or_mgr_v_pool(ref, l), pool_elems * 2) == 0, "V pages bit-exact");
+    }
+    or_mgr_destroy(ref);
+    return ok;
+}
+
+bool test_paged_attention_qwen06b() { return run_paged_graph(16, 8, 40, 3, 0x5EED0001); }
+bool test_paged_attention_qwen4b() { return run_paged_graph(32, 8, 33, 3, 0x5EED0003); }
+
+bool test_paged_attention_errors() {
+    MemoryManager mm;
+    PagedAttentionManager& pam = mm.create_attention_manager(Device::HIP, 0, 8 << 20);
+    pam.init_layer(0, 2, 64, DataType::GGML_TYPE_BF16);
+    pam.reserve_layer(0, 8);
+    DevBuf q(4 * 64 * 2), k(2 * 64 * 2), o(4 * 64 * 2);
+    (void)fill_normal(q, 7);
+    (void)fill_normal(k, 8);
+    Tensor Q = make_tensor(q.p, {1, 4, 1, 64}), K = make_tensor(k.p, {1, 2, 1, 64});
+    Tensor out = make_tensor(o.p, {1, 4, 1, 64});
+    out.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+    out.src = {&Q, &K, &K, nullptr, nullptr, nullptr};
+    out.op_params = {64.0f, 0.125f, 1.0f, 2.0f};
+    out.layer_id = 0;
+    bool threw = false;
+    try {
+        kernel::paged_attention(&out, 0);  // attention.cu:511 throws for head_dim != 128
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    ASSERT(threw, "head_dim 64 throws std::runtime_error");
+    // inactive layer: silent return, output untouched (attention.cpp:127)
+    std::vector<uint16_t> sentinel(4 * 64, 0x7777);
+    to_device(o.p, sentinel);
+    out.layer_id = 5;
+    kernel::paged_attention(&out, 0);
+    ASSERT(to_host<uint16_t>(o.p, sentinel.size()) == sentinel, "inactive layer leaves out untouched");
+    // a CPU node never reaches the HIP backend
+    out.device = Device::CPU;
+    threw = false;
+    try {
+        kernel::paged_attention(&out, 0);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    ASSERT(threw, "dispatchOp throws for a device this library does not serve");
+    return true;
+}
+
+// ----------------------------------------------- FlashAttention (non-paged)
+bool run_flash(int32_t B, int32_t Hq, int32_t Hkv, int32_t S, bool causal, uint64_t seed) {
+    const int32_t D = 128, G = Hq / Hkv;
+    const float scale = 1.0f / std::sqrt(float(D));
+    DevBuf q(size_t(B) * Hq * S * D * 2), k(size_t(B) * Hkv * S * D * 2), v(size_t(B) * Hkv * S * D * 2),
+        o(size_t(B) * Hq * S * D * 2);
+    auto hq = fill_normal(q, seed), hk = fill_normal(k, seed + 1), hv = fill_normal(v, seed + 2);
+    Tensor Q = make_tensor(q.p, {B, Hq, S, D}), K = make_tensor(k.p, {B, Hkv, S, D}),
+           V = make_tensor(v.p, {B, Hkv, S, D});
+    Tensor out = make_tensor(o.p, {B, Hq, S, D});
+    out.op_type = OperationType::OP_TYPE_FLASH_ATTN;
+    out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
+    out.op_params = {float(D), scale, causal ? 1.0f : 0.0f, float(G)};
+    ASSERT(kernel::dispatch(&out, 0), "executor dispatches FLASH_ATTN");
+    std::vector<uint16_t> want(size_t(B) * Hq * S * D);
+    or_flash_attention(hq.data(), hk.data(), hv.data(), want.data(), B, Hq, S, Hkv, D, G, scale, causal);
+    char what[96];
+    std::snprintf(what, sizeof what, "flash B%d Hq%d Hkv%d S%d causal %d", B, Hq, Hkv, S, int(causal));
+    return attn_close(to_host<uint16_t>(o.p, want.size()), want, what);
+}
+
+bool test_flash_attention_causal() { return run_flash(2, 8, 2, 77, true, 11); }
+bool test_flash_attention_full() { return run_flash(1, 16, 8, 130, false, 12); }
+bool test_flash_attention_one_token() { return run_flash(1, 4, 4, 1, true, 13); }
+
+// ----------------------------------------------------- RMSNorm, RoPE, tables
+bool test_rms_norm_rope_nodes() {
+    const int32_t H = 5, S = 9, D = 128, max_seq = 64;
+    const int64_t start = 7;
+    MemoryManager mm;
+    DevBuf x(size_t(H) * S * D * 2), y(size_t(H) * S * D * 2), r(size_t(H) * S * D * 2), w(D * 4);
+    DevBuf cs(size_t(max_seq) * D * 4), sn(size_t(max_seq) * D * 4);
+    auto hx = fill_normal(x, 21);
+    std::vector<float> gamma(D);
+    for (int i = 0; i < D; ++i) gamma[i] = 0.5f + float(i) / D;
+    to_device(w.p, gamma);
+
+    Tensor X = make_tensor(x.p, {1, H, S, D}), W = make_tensor(w.p, {D, 0, 0, 0}, DataType::GGML_TYPE_F32);
+    Tensor norm = make_tensor(y.p, {1, H, S, D});
+    norm.op_type = OperationType::OP_TYPE_RMS_NORM;
+    norm.src = {&X, &W, nullptr, nullptr, nullptr, nullptr};
+    norm.op_params = {1e-6f, 0, 0, 0};
+    Tensor cos_t = make_tensor(cs.p, {max_seq, D, 0, 0}, DataType::GGML_TYPE_F32),
+           sin_t = make_tensor(sn.p, {max_seq, D, 0, 0}, DataType::GGML_TYPE_F32);
+    cos_t.op_type = sin_t.op_type = OperationType::OP_TYPE_ROPE_CACHE;
+    cos_t.op_params = sin_t.op_params = {1e6f, float(D), float(max_seq), 0};
+    cos_t.name = "rope_cos";
+    sin_t.name = "rope_sin";
+    Tensor rope = make_tensor(r.p, {1, H, S, D});
+    rope.op_type = OperationType::OP_TYPE_APPLY_ROPE;
+    rope.src = {&norm, &cos_t, &sin_t, nullptr, nullptr, nullptr};
+    rope.op_params = {float(D), float(D), float(start), 0};
+    for (Tensor* t : {&norm, &cos_t, &sin_t, &rope}) ASSERT(kernel::dispatch(t, 0), "dispatched");
+
+    std::vector<float> rc(size_t(max_seq) * D), rs(size_t(max_seq) * D);
+    or_rope_cache(rc.data(), 1e6f, D, max_seq, 1);
+    or_rope_cache(rs.data(), 1e6f, D, max_seq, 0);
+    ASSERT(to_host<float>(cs.p, rc.size()) == rc, "cos table bit-exact");
+    ASSERT(to_host<float>(sn.p, rs.size()) == rs, "sin table bit-exact");
+    std::vector<uint16_t> yn(hx.size()), yr(hx.size());
+    or_rms_norm(yn.data(), hx.data(), gamma.data(), size_t(H) * S, D, 1e-6f);
+    ASSERT(to_host<uint16_t>(y.p, yn.size()) == yn, "rms_norm bit-exact");
+    or_apply_rope(yr.data(), yn.data(), rc.data(), rs.data(), H, S, D, start);
+    ASSERT(to_host<uint16_t>(r.p, yr.size()) == yr, "apply_rope bit-exact");
+    return true;
+}
+
+}  // namespace
+
+int main() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        std::printf("no HIP device\n");
+        return 2;
+    }
+    return run_tests({
+        {"device enum", test_device_enum},
+        {"block_pool alloc/free", test_block_pool_alloc_free},
+        {"block_pool many allocs", test_block_pool_many_allocs},
+        {"block_pool reset", test_block_pool_reset},
+        {"page_table append_kv", test_page_table_append_kv},
+        {"page_table multi layer", test_page_table_multi_layer},
+        {"kv_cache_per_layer switch + sizing", test_kv_cache_per_layer_switch},
+        {"paged attention graph Qwen3-0.6B shape", test_paged_attention_qwen06b},
+        {"paged attention graph Qwen3-4B shape", test_paged_attention_qwen4b},
+        {"paged attention errors", test_paged_attention_errors},
+        {"flash attention causal", test_flash_attention_causal},
+        {"flash attention full", test_flash_attention_full},
+        {"flash attention one token", test_flash_attention_one_token},
+        {"rms_norm / rope_cache / apply_rope nodes", test_rms_norm_rope_nodes},
+    });
+}

@@ -1,0 +1,90 @@
+"""Non-paged attention (FlashAttentionImpl, src/backend/cpu/attention.cpp:39-121;
+the op type of kv_cache_per_layer = 0) on the GPU, through
+genllm_flash_attention, against the CPU oracle (small shapes) and a float32
+torch reference (prefill size).  Tolerance: max-abs <= 2^-7 * max|ref|,
+relative L2 <= 1e-2."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import assert_attn_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(synth, seed, B, Hq, Hkv, S, D=128):
+    q = synth.normal_bf16(seed, (B, Hq, S, D))
+    k = synth.normal_bf16(seed, (B, Hkv, S, D), offset=1 << 26)
+    v = synth.normal_bf16(seed, (B, Hkv, S, D), offset=2 << 26)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,causal", [
+    (2, 8, 2, 77, True),     # GQA 4:1, ragged last page, two batch entries
+    (1, 16, 8, 130, False),  # no mask: every query sees all 130 keys
+    (1, 4, 4, 1, True),      # one token: out = v
+    (1, 16, 8, 16, True),    # exactly one page
+])
+def test_flash_vs_oracle(orc, B, Hq, Hkv, S, causal):
+    import torch
+
+    from genllm_amd import paged, synth
+
+    print(f"flash B{B} Hq{Hq} Hkv{Hkv} S{S} causal={causal}", flush=True)
+    scale = 1.0 / np.sqrt(128)
+    q, k, v = _inputs(synth, 900 + S, B, Hq, Hkv, S)
+    out = torch.empty((B, Hq, S, 128), dtype=torch.bfloat16, device="cuda")
+    paged.flash_attention(paged.to_device_bf16(q), paged.to_device_bf16(k), paged.to_device_bf16(v), out,
+                          Hq // Hkv, scale, causal)
+    torch.cuda.synchronize()
+    want = orc.flash_attention(q, k, v, Hq // Hkv, scale, causal)
+    got = paged.to_host_bits(out)
+    assert_attn_close(got, want, f"flash S{S}")
+    if S == 1:
+        # a single key: softmax weight 1, the output is that key's V row, exactly
+        assert np.array_equal(got[0, :, 0, :], v[0, np.arange(Hq) // (Hq // Hkv), 0, :])
+
+
+def test_flash_prefill_size_vs_torch():
+    """Qwen3-1.7B prefill shape (config 4 without paging): 2048 tokens, 16 q
+    heads over 8 kv heads, causal; heads 0, 1 and 15 against float32 torch."""
+    import torch
+
+    from genllm_amd import paged, synth
+
+    B, Hq, Hkv, S, D = 1, 16, 8, 2048, 128
+    print("flash prefill 2048", flush=True)
+    scale = 1.0 / np.sqrt(D)
+    q = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    k = torch.empty((B, Hkv, S, D), dtype=torch.bfloat16, device="cuda")
+    v = torch.empty_like(k)
+    for i, t in enumerate((q, k, v)):
+        paged.fill_normal_bf16(t, synth.config_seed(4) + 70 + i)
+    out = torch.empty_like(q)
+    paged.flash_attention(q, k, v, out, Hq // Hkv, scale, True)
+    torch.cuda.synchronize()
+    qf, kf, vf = (t.float().cpu() for t in (q, k, v))
+    mask = torch.triu(torch.ones(S, S, dtype=torch.bool), 1)
+    for h in (0, 1, 15):
+        s = (qf[0, h] @ kf[0, h // 2].T) * scale
+        s.masked_fill_(mask, float("-inf"))
+        ref = torch.softmax(s, dim=-1) @ vf[0, h // 2]
+        want = ref.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert_attn_close(paged.to_host_bits(out[0, h]), want, f"flash 2048 head {h}")
+
+
+def test_flash_rejects_bad_shapes():
+    import torch
+
+    from genllm_amd import paged
+    from genllm_amd._lib import GenllmError
+
+    q = torch.zeros((1, 4, 8, 64), dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros((1, 2, 8, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(GenllmError):  # head_dim 64: unsupported, as the CUDA op throws
+        paged.flash_attention(q, k, k, torch.empty_like(q), 2, 0.125)
+    q = torch.zeros((1, 6, 8, 128), dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros((1, 4, 8, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(GenllmError):  # 6 q heads cannot map onto 4 kv heads with groups 2
+        paged.flash_attention(q, k, k, torch.empty_like(q), 2, 0.125)
