@@ -7,14 +7,19 @@
 
 namespace genllm {
 
-// Device page-table entries opened by this call, passed by value so that the
-// scatter needs no prior copy (decode opens at most one page per step).
-struct TableUpdate {
+// Device page-table entries opened by this call, passed by value in the launch
+// arguments so that no copy precedes the kernel; the kernel writes them into
+// the device table.
+template <int N>
+struct TableUpdateN {
     int32_t first = 0;
     int32_t count = 0;
-    int32_t k[4] = {0, 0, 0, 0};
-    int32_t v[4] = {0, 0, 0, 0};
+    int32_t k[N] = {};
+    int32_t v[N] = {};
 };
+using TableUpdate = TableUpdateN<4>;  // decode step: at most 16 queries open at most 2 pages
+constexpr int kAppendUpdMax = 256;    // append chunk: up to 4096 tokens (2 KiB of ids)
+using AppendTableUpdate = TableUpdateN<kAppendUpdMax>;
 
 struct AppendParams {
     const uint16_t* k = nullptr;
@@ -40,7 +45,8 @@ struct AppendParams {
     int64_t page_elems = 0;   // 16 * Hkv * D
     int32_t* k_ids = nullptr;
     int32_t* v_ids = nullptr;
-    TableUpdate upd;
+    int32_t max_blocks = INT32_MAX;  // ids outside [0, max_blocks) are never written through
+    AppendTableUpdate upd;
 };
 int launch_kv_append(const AppendParams& p, int head_dim, hipStream_t stream);
 

@@ -45,21 +45,32 @@ struct Append {
     static constexpr int R = D / 32;  // 8-byte chunks per q/k row and lane
     static constexpr int U = D / 64;  // 16-byte chunks per v row and lane
 
-    __device__ static int32_t page_id(const AppendParams& p, int lp, int which) {
+    // Block id of local page lp (K: which = 0, V: 1): opened by this call ->
+    // from the launch arguments, else from the device table.  -1 when the id
+    // is outside the pool, so no store can leave it.
+    // Both candidates are loaded from their own address space (launch
+    // arguments, device table) and the value is selected: a pointer select
+    // would make a flat load that waits on every outstanding access.
+    __device__ __forceinline__ static int32_t page_id(const AppendParams& p, int lp, int which) {
         const int rel = lp - p.upd.first;
-        if (rel >= 0 && rel < p.upd.count) return which ? p.upd.v[rel] : p.upd.k[rel];
-        return which ? p.v_ids[lp] : p.k_ids[lp];
+        const bool opened = rel >= 0 && rel < p.upd.count;
+        const int32_t from_args = (which ? p.upd.v : p.upd.k)[opened ? rel : 0];
+        const int32_t from_table = (which ? p.v_ids : p.k_ids)[lp];
+        const int32_t id = opened ? from_args : from_table;
+        return (id >= 0 && id < p.max_blocks) ? id : -1;
     }
 
-    __device__ static uint16_t* k_dst(const AppendParams& p, int tok, int h) {
+    __device__ __forceinline__ static uint16_t* k_dst(const AppendParams& p, int tok, int h) {
         const int gpos = p.pos0 + tok;
         const int64_t id = page_id(p, gpos / kPage, 0);
+        if (id < 0) return nullptr;
         return p.k_pool + id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + h * D;
     }
 
-    // RMSNorm (optional) + RoPE (optional) of one row, in place.
-    __device__ static void norm_rope(uint2 (&x)[R], const float* gamma, float eps, const float* cos_row,
-                                     const float* sin_row, int j) {
+    // RMSNorm (optional, gamma chunks gw) + RoPE (optional, table chunks c4/s4
+    // of the row's position) of one row, in place.
+    __device__ __forceinline__ static void norm_rope(uint2 (&x)[R], bool norm, const float4 (&gw)[R], float eps, bool rope,
+                                     const float4 (&c4)[R / 2], const float4 (&s4)[R / 2]) {
         float v[R][4];
 #pragma unroll
         for (int t = 0; t < R; ++t) {
@@ -68,7 +79,7 @@ struct Append {
             v[t][2] = bf16_lo(x[t].y);
             v[t][3] = bf16_hi(x[t].y);
         }
-        if (gamma) {
+        if (norm) {
             float A[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -89,8 +100,7 @@ struct Append {
             const float r = 1.0f / __builtin_sqrtf(ss / float(D) + eps);
 #pragma unroll
             for (int t = 0; t < R; ++t) {
-                const float4 gw = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * t);
-                const float gv[4] = {gw.x, gw.y, gw.z, gw.w};
+                const float gv[4] = {gw[t].x, gw[t].y, gw[t].z, gw[t].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float y = (v[t][q] * r) * gv[q];
@@ -99,13 +109,11 @@ struct Append {
             }
         }
         uint32_t o[R][4];
-        if (cos_row) {
+        if (rope) {
 #pragma unroll
             for (int t = 0; t < R / 2; ++t) {
-                const float4 c4 = *reinterpret_cast<const float4*>(cos_row + 4 * j + 32 * t);
-                const float4 s4 = *reinterpret_cast<const float4*>(sin_row + 4 * j + 32 * t);
-                const float c[4] = {c4.x, c4.y, c4.z, c4.w};
-                const float s[4] = {s4.x, s4.y, s4.z, s4.w};
+                const float c[4] = {c4[t].x, c4[t].y, c4[t].z, c4[t].w};
+                const float s[4] = {s4[t].x, s4[t].y, s4[t].z, s4[t].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const float x0 = v[t][q], x1 = v[t + R / 2][q];
@@ -153,9 +161,13 @@ struct Append {
         if (kind < 2) {
             const bool is_q = kind == 0;
             const int H = is_q ? p.Hq : p.Hkv;
+            // Every load of the wave is issued before any arithmetic: the rows,
+            // gamma (once) and the RoPE table chunks of each row's position.
             uint2 x[TPW][R];
+            float4 c4[TPW][R / 2], s4[TPW][R / 2];
             int tok[TPW], h[TPW];
             bool ok[TPW];
+            const bool rope = p.cos_tab != nullptr;
 #pragma unroll
             for (int u = 0; u < TPW; ++u) {
                 const int64_t t = t0 + u;
@@ -168,43 +180,57 @@ struct Append {
                 for (int c = 0; c < R; ++c)
                     x[u][c] = ok[u] ? *reinterpret_cast<const uint2*>(src + 4 * j + 32 * c) : make_uint2(0, 0);
             }
+            if (rope) {
+#pragma unroll
+                for (int u = 0; u < TPW; ++u) {
+                    const bool live = t0 + u < n_kind;
+                    const int64_t row = (p.rope_pos0 + (live ? tok[u] : 0)) * p.rope_stride + 4 * j;
+#pragma unroll
+                    for (int c = 0; c < R / 2; ++c) {
+                        c4[u][c] = *reinterpret_cast<const float4*>(p.cos_tab + row + 32 * c);
+                        s4[u][c] = *reinterpret_cast<const float4*>(p.sin_tab + row + 32 * c);
+                    }
+                }
+            }
             const float* gamma = is_q ? p.gamma_q : p.gamma_k;
+            float4 gw[R];
+            if (gamma) {
+#pragma unroll
+                for (int c = 0; c < R; ++c) gw[c] = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * c);
+            }
 #pragma unroll
             for (int u = 0; u < TPW; ++u) {
                 if (t0 + u >= n_kind) break;  // wave-uniform
-                const float* crow = p.cos_tab ? p.cos_tab + (p.rope_pos0 + tok[u]) * p.rope_stride : nullptr;
-                const float* srow = p.sin_tab ? p.sin_tab + (p.rope_pos0 + tok[u]) * p.rope_stride : nullptr;
-                norm_rope(x[u], gamma, p.eps, crow, srow, j);
+                norm_rope(x[u], gamma != nullptr, gw, p.eps, rope, c4[u], s4[u]);
                 if (!ok[u]) continue;
                 uint16_t* dst = is_q ? p.q_out + tok[u] * p.qo_tok_stride + h[u] * p.qo_head_stride
                                      : k_dst(p, tok[u], h[u]);
+                if (!dst) continue;
 #pragma unroll
                 for (int c = 0; c < R; ++c) *reinterpret_cast<uint2*>(dst + 4 * j + 32 * c) = x[u][c];
             }
         } else {
-            uint4 x[TPW][U];
-            uint16_t* dst[TPW];
+            uint4 xv[TPW][U];
+            int64_t dst[TPW];  // element offset in the V pool, -1 = nothing to store
 #pragma unroll
             for (int u = 0; u < TPW; ++u) {
                 const int64_t t = t0 + u;
                 const int tk = int(t / ng);
                 const int hh = int(t - int64_t(tk) * ng) * 8 + r;
                 const bool ok = t < n_kind && hh < p.Hkv;
-                dst[u] = nullptr;
-                if (ok) {
-                    const uint16_t* src = p.v + tk * p.v_tok_stride + hh * p.v_head_stride;
+                const uint16_t* src = p.v + tk * p.v_tok_stride + hh * p.v_head_stride;
 #pragma unroll
-                    for (int c = 0; c < U; ++c) x[u][c] = *reinterpret_cast<const uint4*>(src + 8 * j + 64 * c);
-                    const int gpos = p.pos0 + tk;
-                    const int64_t id = page_id(p, gpos / kPage, 1);
-                    dst[u] = p.v_pool + id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + hh * D;
-                }
+                for (int c = 0; c < U; ++c)
+                    xv[u][c] = ok ? *reinterpret_cast<const uint4*>(src + 8 * j + 64 * c) : make_uint4(0, 0, 0, 0);
+                const int gpos = p.pos0 + tk;
+                const int64_t id = ok ? page_id(p, gpos / kPage, 1) : -1;
+                dst[u] = id >= 0 ? id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + hh * D : -1;
             }
 #pragma unroll
             for (int u = 0; u < TPW; ++u)
-                if (dst[u])
+                if (dst[u] >= 0)
 #pragma unroll
-                    for (int c = 0; c < U; ++c) *reinterpret_cast<uint4*>(dst[u] + 8 * j + 64 * c) = x[u][c];
+                    for (int c = 0; c < U; ++c) *reinterpret_cast<uint4*>(p.v_pool + dst[u] + 8 * j + 64 * c) = xv[u][c];
         }
     }
 };

@@ -86,6 +86,11 @@ struct LayerState {
     uint16_t* v_base = nullptr;
     int32_t* d_k_ids = nullptr;
     int32_t* d_v_ids = nullptr;
+    // Pinned host staging of the table ([max_blocks] K ids, then [max_blocks]
+    // V ids): new entries are written here once and uploaded asynchronously,
+    // so an append never waits on a pageable copy.  An entry is rewritten only
+    // after reset / set_page_table, which first drain pending uploads.
+    int32_t* h_ids = nullptr;
     int32_t max_blocks = 0;
     size_t block_bytes = 0;
 };
@@ -101,6 +106,8 @@ struct genllm_kv {
     std::map<int32_t, LayerState> layers;
     void* ws = nullptr;    // split-K decode workspace (per-split partials)
     size_t ws_bytes = 0;
+    std::vector<void*> pinned;     // every h_ids buffer, freed at destroy
+    bool uploads_pending = false;  // async table uploads from h_ids may be in flight
 };
 
 namespace {
@@ -131,10 +138,13 @@ int64_t pages_opened(int32_t num_cached, int32_t count) {
 }
 
 // append_kv_pages (page_attention.cpp:141-162) on the host state.  New entries
-// go to the device table either through `upd` (when given and small enough) or
-// with an async copy on `stream`.
-int append_pages(LayerState& s, int32_t count, hipStream_t stream, TableUpdate* upd) {
-    if (upd) *upd = TableUpdate{};
+// go to the device table either through `upd` (the next kernel writes them;
+// when given and large enough) or with async copies on `stream` from the
+// layer's pinned staging.
+template <typename Upd = TableUpdate>
+int append_pages(genllm_kv* kv, LayerState& s, int32_t count, hipStream_t stream, Upd* upd = nullptr) {
+    constexpr size_t kCap = sizeof(Upd::k) / sizeof(int32_t);
+    if (upd) *upd = Upd{};
     if (!s.active || count <= 0) return GENLLM_OK;
     const int64_t need = pages_opened(s.num_cached, count);
     if (need > s.k_pool.available() || need > s.v_pool.available())
@@ -158,7 +168,7 @@ int append_pages(LayerState& s, int32_t count, hipStream_t stream, TableUpdate* 
         if (new_size > size_t(s.max_blocks))
             return fail(GENLLM_ERR_POOL_FULL, "append_kv_pages: page table longer than max_blocks");
         const size_t n = new_size - old_size;
-        if (upd && n <= 4) {
+        if (upd && n <= kCap) {
             upd->first = int32_t(old_size);
             upd->count = int32_t(n);
             for (size_t i = 0; i < n; ++i) {
@@ -166,10 +176,13 @@ int append_pages(LayerState& s, int32_t count, hipStream_t stream, TableUpdate* 
                 upd->v[i] = s.v_ids[old_size + i];
             }
         } else {
-            GENLLM_HIP_TRY(hipMemcpyAsync(s.d_k_ids + old_size, s.k_ids.data() + old_size, n * sizeof(int32_t),
-                                          hipMemcpyHostToDevice, stream));
-            GENLLM_HIP_TRY(hipMemcpyAsync(s.d_v_ids + old_size, s.v_ids.data() + old_size, n * sizeof(int32_t),
-                                          hipMemcpyHostToDevice, stream));
+            int32_t* hk = s.h_ids + old_size;
+            int32_t* hv = s.h_ids + s.max_blocks + old_size;
+            std::copy(s.k_ids.begin() + old_size, s.k_ids.end(), hk);
+            std::copy(s.v_ids.begin() + old_size, s.v_ids.end(), hv);
+            kv->uploads_pending = true;
+            GENLLM_HIP_TRY(hipMemcpyAsync(s.d_k_ids + old_size, hk, n * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+            GENLLM_HIP_TRY(hipMemcpyAsync(s.d_v_ids + old_size, hv, n * sizeof(int32_t), hipMemcpyHostToDevice, stream));
         }
     }
     return GENLLM_OK;
@@ -193,6 +206,15 @@ int ensure_workspace(genllm_kv* kv, size_t need) {
     }
     GENLLM_HIP_TRY(hipMalloc(&kv->ws, need));
     kv->ws_bytes = need;
+    return GENLLM_OK;
+}
+
+// Waits for async table uploads that read the pinned staging.
+int drain_uploads(genllm_kv* kv) {
+    if (!kv->uploads_pending) return GENLLM_OK;
+    GENLLM_HIP_TRY(hipSetDevice(kv->device));
+    GENLLM_HIP_TRY(hipDeviceSynchronize());
+    kv->uploads_pending = false;
     return GENLLM_OK;
 }
 
@@ -270,6 +292,7 @@ extern "C" int genllm_kv_destroy(genllm_kv* kv) {
     (void)hipDeviceSynchronize();
     if (kv->base) (void)hipFree(kv->base);
     if (kv->ws) (void)hipFree(kv->ws);
+    for (void* h : kv->pinned) (void)hipHostFree(h);
     delete kv;
     return GENLLM_OK;
 }
@@ -300,6 +323,11 @@ extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max
     if (int rc = pool_allocate(kv, total, 256, &vp)) return rc;
     if (int rc = pool_allocate(kv, size_t(max_blocks) * 4, 256, &ki)) return rc;
     if (int rc = pool_allocate(kv, size_t(max_blocks) * 4, 256, &vi)) return rc;
+    void* staging = nullptr;
+    GENLLM_HIP_TRY(hipSetDevice(kv->device));
+    GENLLM_HIP_TRY(hipHostMalloc(&staging, size_t(max_blocks) * 2 * sizeof(int32_t), hipHostMallocDefault));
+    kv->pinned.push_back(staging);
+    s.h_ids = static_cast<int32_t*>(staging);
     s.k_base = static_cast<uint16_t*>(kp);
     s.v_base = static_cast<uint16_t*>(vp);
     s.d_k_ids = static_cast<int32_t*>(ki);
@@ -322,11 +350,12 @@ extern "C" int genllm_kv_is_active(genllm_kv* kv, int32_t layer, int32_t* active
 extern "C" int genllm_kv_append_pages(genllm_kv* kv, int32_t layer, int32_t count, void* stream) {
     if (!kv) return fail(GENLLM_ERR_INVALID, "append_pages: null kv");
     LayerState& s = kv->layers[layer];
-    return append_pages(s, count, as_stream(stream), nullptr);
+    return append_pages<TableUpdate>(kv, s, count, as_stream(stream), nullptr);
 }
 
 extern "C" int genllm_kv_reset(genllm_kv* kv) {
     if (!kv) return fail(GENLLM_ERR_INVALID, "reset: null kv");
+    if (int rc = drain_uploads(kv)) return rc;  // staged entries are about to be reused
     for (auto& [id, s] : kv->layers) {
         s.num_cached = 0;
         s.k_ids.clear();
@@ -387,6 +416,7 @@ extern "C" int genllm_kv_set_page_table(genllm_kv* kv, int32_t layer, const int3
     for (int32_t i = 0; i < n; ++i)
         if (k_ids[i] < 0 || k_ids[i] >= s->k_pool.num_blocks || v_ids[i] < 0 || v_ids[i] >= s->v_pool.num_blocks)
             return fail(GENLLM_ERR_INVALID, "set_page_table: id was never handed out by its pool");
+    if (int rc = drain_uploads(kv)) return rc;  // later appends rewrite staged entries
     s->k_ids.assign(k_ids, k_ids + n);
     s->v_ids.assign(v_ids, v_ids + n);
     s->num_cached = num_cached;
@@ -442,7 +472,7 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     const int32_t pos0 = s->num_cached;
     const bool fuse = int64_t(n_kv_groups) * seq_len <= 16;
     AppendParams ap;
-    if (int rc = append_pages(*s, seq_len, st, &ap.upd)) return rc;
+    if (int rc = append_pages(kv, *s, seq_len, st, &ap.upd)) return rc;
     ap.k = static_cast<const uint16_t*>(k);
     ap.v = static_cast<const uint16_t*>(v);
     ap.k_tok_stride = ap.v_tok_stride = head_dim;
@@ -456,6 +486,7 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     ap.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
     ap.k_ids = s->d_k_ids;
     ap.v_ids = s->d_v_ids;
+    ap.max_blocks = s->max_blocks;
     if (!fuse)
         if (int rc = launch_kv_append(ap, head_dim, st)) return rc;
     if (s->k_ids.empty()) return GENLLM_OK;  // attention.cpp:148
@@ -492,7 +523,15 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
         p.v_pool_w = s->v_base;
         p.k_ids_w = s->d_k_ids;
         p.v_ids_w = s->d_v_ids;
-        p.upd = ap.upd;
+        // seq_len <= 16 opens at most 2 pages
+        if (ap.upd.count > int32_t(sizeof(p.upd.k) / sizeof(int32_t)))
+            return fail(GENLLM_ERR_INVALID, "paged_attention: too many pages opened for the fused append");
+        p.upd.first = ap.upd.first;
+        p.upd.count = ap.upd.count;
+        for (int32_t i = 0; i < ap.upd.count; ++i) {
+            p.upd.k[i] = ap.upd.k[i];
+            p.upd.v[i] = ap.upd.v[i];
+        }
     }
     return run_attention(p, head_dim, s->max_blocks, st, kv);
 }
@@ -526,7 +565,7 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     hipStream_t st = as_stream(stream);
     AppendParams ap;
     const int32_t pos0 = s->num_cached;
-    if (int rc = append_pages(*s, seq_len, st, &ap.upd)) return rc;
+    if (int rc = append_pages(kv, *s, seq_len, st, &ap.upd)) return rc;
     ap.k = static_cast<const uint16_t*>(k);
     ap.k_tok_stride = k_tok_stride;
     ap.k_head_stride = k_head_stride;
@@ -557,6 +596,7 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     ap.page_elems = int64_t(kPage) * s->n_kv_heads * D;
     ap.k_ids = s->d_k_ids;
     ap.v_ids = s->d_v_ids;
+    ap.max_blocks = s->max_blocks;
     return launch_kv_append(ap, D, st);
 }
 
