@@ -47,10 +47,14 @@ namespace {
 constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
 constexpr int kWaves = 4;
 constexpr int kMaxSplits = 256;
-constexpr int PF = 4;          // pages in flight per wave
+constexpr int PF = 3;          // pages in flight per wave (3: two waves per SIMD fit)
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource word 3 for raw (untyped) buffer accesses on gfx9-family
+// GPUs: 32-bit data format, no swizzle, no index addressing.
+constexpr int kBufferFlags = 0x00020000;
 
 __device__ __forceinline__ f32x4_t mfma16x16x16(const s16x4_t& a, const s16x4_t& b, const f32x4_t& c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
@@ -116,28 +120,52 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
             my_vid = p.v_ids[pg];
         }
     }
-    const int64_t kcol = h * D + n16 * p.kv_row + 8 * g;        // element offsets inside a page
-    const int64_t vcol = h * D + (4 * g) * p.kv_row + 8 * n16;
+    // Element offsets inside a page (< 2^31): lane's K operand chunk (token
+    // n16, dims 8g + 32c) and V row chunk (token 4g + i, dims 8 n16).  Page
+    // bases are wave-uniform, so a load is a scalar base plus this offset.
+    const uint32_t kcol = uint32_t(h * D + n16 * p.kv_row + 8 * g);
+    const uint32_t vcol = uint32_t(h * D + 4 * g * p.kv_row + 8 * n16);
+    const int kcol_b = int(2 * kcol), vcol_b = int(2 * vcol);  // the same in bytes
+    const int kv_row_b = int(2 * p.kv_row), page_bytes = int(2 * p.page_elems);
     const bool fused = p.k_new != nullptr;
     uint16_t* vt = lds_vt[wv];
+    // Pages from special_from on hold the end of the cache: keys a query may
+    // not see (causal), slots past n_cached and, in the fused op, the appended
+    // tokens.  Only they take the per-token conditions below.
+    const int lo_tok = min(p.causal ? p.n_cached - p.S + 1 : p.n_cached, p.new_from);
+    const int special_from = lo_tok / kPage;
+    auto page_of = [&](int j) { return begin + wv + kWaves * j; };
 
     // Token t >= new_from is this call's append: read it from k_new / v_new.
-    auto load_page = [&](int j, PageRegs& pr) {
-        const int pg = begin + wv + kWaves * j;
-        const int64_t kid = __builtin_amdgcn_readlane(my_kid, j);
-        const int64_t vid = __builtin_amdgcn_readlane(my_vid, j);
-        const uint16_t* kb = p.k_pool + kid * p.page_elems + kcol;
-        const uint16_t* vb = p.v_pool + vid * p.page_elems + vcol;
+    auto load_page = [&](int j, PageRegs& pr, bool special) {
+        const int pg = page_of(j);
+        const uint16_t* kb = p.k_pool + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
+        const uint16_t* vb = p.v_pool + int64_t(__builtin_amdgcn_readlane(my_vid, j)) * p.page_elems;
+        if (!special) {
+            // buffer loads: scalar page base in the resource (whose size bounds
+            // every lane offset), 32-bit lane offset, row offset as immediate
+            // (K) or scalar offset (V)
+            const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kb), 0, page_bytes, kBufferFlags);
+            const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb), 0, page_bytes, kBufferFlags);
+#pragma unroll
+            for (int c = 0; c < KS; ++c)
+                pr.k[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, kcol_b + 64 * c, 0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                pr.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vcol_b, i * kv_row_b, 0));
+            return;
+        }
+        const uint16_t* kr = kb + kcol;
         if (fused) {
             const int tk = pg * kPage + n16;
             if (tk >= p.new_from && tk < p.n_cached)
-                kb = p.k_new + h * p.new_head_stride + int64_t(tk - p.new_from) * p.new_tok_stride + 8 * g;
+                kr = p.k_new + h * p.new_head_stride + int64_t(tk - p.new_from) * p.new_tok_stride + 8 * g;
         }
 #pragma unroll
-        for (int c = 0; c < KS; ++c) pr.k[c] = *reinterpret_cast<const uint4*>(kb + 32 * c);
+        for (int c = 0; c < KS; ++c) pr.k[c] = *reinterpret_cast<const uint4*>(kr + 32 * c);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint16_t* src = vb + i * p.kv_row;
+            const uint16_t* src = vb + i * p.kv_row + vcol;
             if (fused) {
                 const int tv = pg * kPage + 4 * g + i;
                 if (tv >= p.new_from && tv < p.n_cached)
@@ -148,21 +176,20 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
     };
     // ... and write the appended rows into their page slots (bit-exact copies)
     auto store_new = [&](int j, const PageRegs& pr) {
-        const int pg = begin + wv + kWaves * j;
+        const int pg = page_of(j);
         if (pg * kPage + kPage <= p.new_from) return;  // wave-uniform: no new token in this page
-        const int64_t kid = __builtin_amdgcn_readlane(my_kid, j);
-        const int64_t vid = __builtin_amdgcn_readlane(my_vid, j);
+        uint16_t* kb = p.k_pool_w + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
+        uint16_t* vb = p.v_pool_w + int64_t(__builtin_amdgcn_readlane(my_vid, j)) * p.page_elems;
         const int tk = pg * kPage + n16;
         if (tk >= p.new_from && tk < p.n_cached) {
-            uint16_t* dst = p.k_pool_w + kid * p.page_elems + kcol;
 #pragma unroll
-            for (int c = 0; c < KS; ++c) *reinterpret_cast<uint4*>(dst + 32 * c) = pr.k[c];
+            for (int c = 0; c < KS; ++c) *reinterpret_cast<uint4*>(kb + kcol + 32 * c) = pr.k[c];
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tv = pg * kPage + 4 * g + i;
             if (tv >= p.new_from && tv < p.n_cached)
-                *reinterpret_cast<uint4*>(p.v_pool_w + vid * p.page_elems + vcol + i * p.kv_row) = pr.v[i];
+                *reinterpret_cast<uint4*>(vb + i * p.kv_row + vcol) = pr.v[i];
         }
     };
 
@@ -171,15 +198,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute_page = [&](int j, const PageRegs& pr) {
-        const int pg = begin + wv + kWaves * j;
-        const int tok0 = pg * kPage + 4 * g;  // this lane's 4 keys: tok0 .. tok0+3
+    auto compute_page = [&](int j, const PageRegs& pr, bool special) {
+        const int tok0 = page_of(j) * kPage + 4 * g;  // this lane's 4 keys: tok0 .. tok0+3
         // V^T into LDS first (its latency hides behind the S^T MFMAs)
         uint4 v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             v[i] = pr.v[i];
-            if (tok0 + i >= p.n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots of the last page
+            if (special && tok0 + i >= p.n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots
         }
         const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
                                   {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
@@ -196,19 +222,22 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < KS; ++c) s = mfma16x16x32(as_bf16x8(pr.k[c]), qb[c], s);
-        float x[4], mx = -INFINITY;
+        // Rows past rows_total have q = 0 (score 0) and are never written out.
+        float x[4], lmx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = tok0 + i;
-            x[i] = (row_ok && t < p.n_cached && t <= qabs) ? s[i] * p.scale_log2 : -INFINITY;
-            mx = fmaxf(mx, x[i]);
+            x[i] = (!special || (t < p.n_cached && t <= qabs)) ? s[i] * p.scale_log2 : -INFINITY;
+            lmx = fmaxf(lmx, x[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
         // Lazy rescale: the row's reference max m_run only moves (and o, l are
         // rescaled) when the page max exceeds it by more than 2^8, so p <= 256.
-        const bool grow = mx > m_run + 8.0f;
-        if (__any(grow)) {
+        // A lane's own 4 keys decide whether any row may grow; the row max
+        // (two cross-lane steps) is formed only then.
+        if (__any(lmx > m_run + 8.0f)) {
+            float mx = fmaxf(lmx, __shfl_xor(lmx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool grow = mx > m_run + 8.0f;
             const float mn = grow ? mx : m_run;
             const float alpha = grow ? exp2_fast(m_run - mn) : 1.0f;
             l_run *= alpha;
@@ -237,18 +266,28 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
         __builtin_amdgcn_wave_barrier();
     };
 
+    auto load_any = [&](int j, PageRegs& pr) {
+        if (page_of(j) >= special_from)
+            load_page(j, pr, true);
+        else
+            load_page(j, pr, false);
+    };
     PageRegs buf[PF];
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u)
-        if (u < np) load_page(u, buf[u]);
+        if (u < np) load_any(u, buf[u]);
     for (int j0 = 0; j0 < np; j0 += PF) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
             const int j = j0 + u;
             if (j < np) {
-                if (j + PF - 1 < np) load_page(j + PF - 1, buf[(u + PF - 1) % PF]);
-                if (fused) store_new(j, buf[u]);
-                compute_page(j, buf[u]);
+                if (j + PF - 1 < np) load_any(j + PF - 1, buf[(u + PF - 1) % PF]);
+                if (page_of(j) >= special_from) {  // wave-uniform
+                    if (fused) store_new(j, buf[u]);
+                    compute_page(j, buf[u], true);
+                } else {
+                    compute_page(j, buf[u], false);
+                }
             }
         }
     }
@@ -260,10 +299,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
         lds_m[wv][n16] = m_run;
         lds_l[wv][n16] = l_run;
     }
+    if (n16 < rows_total) {  // rows past rows_total are never written out
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lds_o[wv][n16][16 * db + 4 * g + i] = acc[db][i];
+            for (int i = 0; i < 4; ++i) lds_o[wv][n16][16 * db + 4 * g + i] = acc[db][i];
+    }
     __syncthreads();
 
     // workgroup merge: wave -> rows ri, ri+4, ...; lane -> dims d2, d2+1
@@ -298,90 +339,75 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
     }
 }
 
-// Merge of the splits: one workgroup per (row, kv head).  Wave w takes splits
-// w, w+4, ... (lane -> 2 dims) and issues the loads of up to 16 of them before
-// reducing the (m, l) of all splits, so the merge costs about one memory round
-// trip; the waves' sums meet in LDS.
+// Merge of the splits: one workgroup per (row, kv head).  Wave w reduces the
+// splits w, w+4, ... to its own log-sum-exp partial (M_w, L_w, O_w): each lane
+// loads the o of its 2 dims and, as a broadcast, the (m, l) of each of those
+// splits, up to 16 splits before any arithmetic (one memory round trip for up
+// to 64 splits); the 4 partials then meet in LDS with the same rule
+//   M = max M_w, L = sum L_w 2^(M_w - M), O = sum O_w 2^(M_w - M), out = O / L.
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
-    constexpr int B = 16;  // o partials in flight per lane
-    __shared__ float part[kWaves][D];
-    __shared__ float s_L;
+    constexpr int U = 16;  // splits in flight per lane
+    __shared__ float s_o[kWaves][D];
+    __shared__ float s_m[kWaves], s_l[kWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ri = blockIdx.x, h = blockIdx.y;
     const int rows = p.G * p.S;
-    const int ns = p.n_splits;  // <= kMaxSplits = 256
+    const int ns = p.n_splits;  // <= kMaxSplits
     const int d2 = lane * 2;
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
                        int64_t(h) * ns * rows + ri;
     const float2* po = reinterpret_cast<const float2*>(p.partial + (int64_t(h) * ns * rows + ri) * D + d2);
     const int64_t sstride = int64_t(rows) * D / 2;  // float2 units between splits
 
-    float2 ov[B];
+    float mw = -INFINITY, lw = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int s0 = wv; s0 < ns; s0 += kWaves * U) {
+        float2 ov[U], mv[U];
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-        const int s2 = wv + kWaves * u;
-        ov[u] = s2 < ns ? po[s2 * sstride] : make_float2(0.0f, 0.0f);
-    }
-    float2 mlv[kMaxSplits / 64];
-#pragma unroll
-    for (int k = 0; k < kMaxSplits / 64; ++k) {
-        const int s2 = lane + 64 * k;
-        mlv[k] = s2 < ns ? ml[s2 * rows] : make_float2(-INFINITY, 0.0f);
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < kMaxSplits / 64; ++k) mx = fmaxf(mx, mlv[k].x);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    auto weight = [&](float m) { return (mx == -INFINITY || m == -INFINITY) ? 0.0f : exp2_fast(m - mx); };
-    if (wv == 0) {
-        float lsum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kMaxSplits / 64; ++k) lsum += mlv[k].y * weight(mlv[k].x);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
-        if (lane == 0) s_L = lsum;
-    }
-    // m of split s2 lives in lane s2 % 64, slot s2 / 64
-    auto m_of = [&](int s2) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < kMaxSplits / 64; ++k) {
-            const float v = __shfl(mlv[k].x, s2 & 63);
-            if ((s2 >> 6) == k) m = v;
+        for (int u = 0; u < U; ++u) {
+            const int s2 = s0 + kWaves * u;
+            ov[u] = s2 < ns ? po[s2 * sstride] : make_float2(0.0f, 0.0f);
+            mv[u] = s2 < ns ? ml[s2 * rows] : make_float2(-INFINITY, 0.0f);
         }
-        return m;
-    };
-    float a0 = 0.0f, a1 = 0.0f;
+        float bm = mw;
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-        const int s2 = wv + kWaves * u;
-        if (s2 < ns) {
-            const float w = weight(m_of(s2));
-            a0 += ov[u].x * w;
-            a1 += ov[u].y * w;
+        for (int u = 0; u < U; ++u) bm = fmaxf(bm, mv[u].x);
+        if (bm == -INFINITY) continue;  // nothing visible yet
+        const float a = mw == -INFINITY ? 0.0f : exp2_fast(mw - bm);
+        lw *= a;
+        o0 *= a;
+        o1 *= a;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float w = mv[u].x == -INFINITY ? 0.0f : exp2_fast(mv[u].x - bm);
+            lw += mv[u].y * w;
+            o0 += ov[u].x * w;
+            o1 += ov[u].y * w;
         }
+        mw = bm;
     }
-    for (int s2 = wv + kWaves * B; s2 < ns; s2 += kWaves) {  // more than 64 splits
-        const float2 v = po[s2 * sstride];
-        const float w = weight(m_of(s2));
-        a0 += v.x * w;
-        a1 += v.y * w;
+    s_o[wv][d2] = o0;
+    s_o[wv][d2 + 1] = o1;
+    if (lane == 0) {
+        s_m[wv] = mw;
+        s_l[wv] = lw;
     }
-    part[wv][d2] = a0;
-    part[wv][d2 + 1] = a1;
     __syncthreads();
     if (wv == 0) {
-        float o0 = 0.0f, o1 = 0.0f;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, s_m[w2]);
+        float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
 #pragma unroll
         for (int w2 = 0; w2 < kWaves; ++w2) {
-            o0 += part[w2][d2];
-            o1 += part[w2][d2 + 1];
+            const float e = s_m[w2] == -INFINITY ? 0.0f : exp2_fast(s_m[w2] - M);
+            L += s_l[w2] * e;
+            O0 += s_o[w2][d2] * e;
+            O1 += s_o[w2][d2 + 1] * e;
         }
-        const float inv = 1.0f / s_L;
+        const float inv = 1.0f / L;
         uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
-        *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(o0 * inv), f32_to_bf16_ref(o1 * inv));
+        *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(O0 * inv), f32_to_bf16_ref(O1 * inv));
     }
 }
 
