@@ -5,9 +5,9 @@
 // at q_abs = n_cached - S + s and attends keys 0..q_abs (causal, :164-181),
 // kv head = q head / groups (:158).
 //
-// Grid (query tiles, Hq), WAVES x 64 threads.  A workgroup owns QW*WAVES
-// consecutive queries of one q head; wave w owns 32 of them (two 16-row
-// MFMA blocks).  K/V tiles of 64 tokens (4 pages) are gathered through the
+// Grid: query tiles x Hq workgroups of WAVES x 64 threads.  A workgroup owns
+// QW*WAVES consecutive queries of one q head; wave w owns QW = 16*NB of them
+// (NB 16-row MFMA blocks).  K/V tiles of 64 tokens (4 pages) are gathered through the
 // block table into LDS:
 //   K  as [token][dim]  (row pad 16 B),
 //   V  transposed as [dim][token] (row pad 8 B) -- pairs of tokens are packed
@@ -23,7 +23,6 @@
 //        lane group g for k-step kt are {32kt+4g+i, 32kt+16+4g+i}, i<4, and
 //        the V^T reads use the same 8 keys).  O^T[dim][q] again belongs to the
 //        lane's own query, so the rescale by 2^(m_old-m_new) is lane-local.
-// Heaviest query tiles are launched first (causal work grows with the tile).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -32,14 +31,16 @@ namespace genllm {
 namespace {
 
 constexpr int KT = 64;  // keys per tile (4 pages)
-constexpr int QW = 32;  // queries per wave
+// 16-row query blocks per wave: 1 keeps a wave at 184 registers, so two
+// workgroups (8 waves) share a CU and the grid's heavy/light pairing applies.
+constexpr int kPrefillBlocks = 1;
 
 __device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
     const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
     return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
-template <int D, int WAVES>
+template <int D, int WAVES, int NB>
 __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p) {
     static_assert(D == 128, "prefill kernel: head_dim 128");
     constexpr int KS = D / 32;     // k-steps of the S^T product
@@ -47,6 +48,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     constexpr int KROW = D + 8;    // K tile row stride (elements)
     constexpr int VROW = KT + 4;   // V^T tile row stride (elements)
     constexpr int NT = WAVES * 64;
+    constexpr int QW = 16 * NB;  // queries per wave: NB blocks of 16 rows
     constexpr int QT = QW * WAVES;
 
     __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * KT * KROW];  // two buffers
@@ -54,17 +56,24 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n16 = lane & 15, g = lane >> 4;
+    // Grid order pairs heavy and light causal tiles: the first half of the
+    // workgroups takes query tiles from the last (most keys) downwards, the
+    // second half from the first upwards, so workgroups b and b + half --
+    // resident together when the dispatcher deals them out round-robin -- sum
+    // to the same work.
     const int n_qt = (p.S + QT - 1) / QT;
-    const int qt = n_qt - 1 - int(blockIdx.x);
-    const int hq = blockIdx.y;
+    const int rank = int(blockIdx.x) / p.Hq;
+    const int hq = int(blockIdx.x) - rank * p.Hq;
+    const int heavy = (n_qt + 1) / 2;
+    const int qt = rank < heavy ? n_qt - 1 - rank : rank - heavy;
     const int hkv = hq / p.G;
     const int qabs0 = p.n_cached - p.S;   // absolute position of query 0
     const int q0 = qt * QT + wv * QW;     // first query of this wave
 
     // Q^T operands (B): lane -> query q0 + 16nb + n16, dims 32ks + 8g..+7
-    bf16x8_t qb[2][KS];
+    bf16x8_t qb[NB][KS];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
         const int s = q0 + 16 * nb + n16;
         const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(s) * p.q_tok_stride;
 #pragma unroll
@@ -75,12 +84,14 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         }
     }
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-    f32x4_t acc[DB][2];
+    float m[NB], l[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) m[nb] = -INFINITY, l[nb] = 0.0f;
+    f32x4_t acc[DB][NB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[db][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int nb = 0; nb < NB; ++nb) acc[db][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int wg_last = min(qt * QT + QT, p.S) - 1;
     const int kv_end = p.causal ? min(qabs0 + wg_last + 1, p.n_cached) : p.n_cached;
@@ -192,11 +203,11 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         const uint16_t* v_cur = v_lds + (t & 1) * (D * VROW);
 
         // ---- S^T = K Q^T
-        f32x4_t s[4][2];
+        f32x4_t s[4][NB];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) s[mb][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int nb = 0; nb < NB; ++nb) s[mb][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -204,7 +215,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
                 const bf16x8_t a =
                     as_bf16x8(*reinterpret_cast<const uint4*>(&k_cur[(16 * mb + n16) * KROW + 32 * ks + 8 * g]));
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) s[mb][nb] = mfma16x16x32(a, qb[nb][ks], s[mb][nb]);
+                for (int nb = 0; nb < NB; ++nb) s[mb][nb] = mfma16x16x32(a, qb[nb][ks], s[mb][nb]);
             }
 
         // ---- online softmax, per lane = per query row
@@ -213,9 +224,9 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         // rescaled) when the tile max exceeds it by more than 2^8, so p <= 256.
         // max over raw scores (scale >= 0), then p = exp2(s * scale*log2e - m), one fma
         const float c = p.scale_log2;
-        float mx[2];
+        float mx[NB];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
+        for (int nb = 0; nb < NB; ++nb) {
             const int qpos = qabs0 + q0 + 16 * nb + n16;
             float mr = -INFINITY;
 #pragma unroll
@@ -228,16 +239,20 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
                     }
                     mr = fmaxf(mr, s[mb][nb][i]);
                 }
-            mr = fmaxf(mr, __shfl_xor(mr, 16));
-            mr = fmaxf(mr, __shfl_xor(mr, 32));
-            mx[nb] = mr == -INFINITY ? -INFINITY : mr * c;
+            mx[nb] = mr == -INFINITY ? -INFINITY : mr * c;  // this lane's 16 keys
         }
-        const bool grow0 = mx[0] > m[0] + 8.0f, grow1 = mx[1] > m[1] + 8.0f;
-        if (__any(grow0 || grow1)) {
-            float alpha[2];
+        // A lane's own keys decide whether any row may grow; the row max (two
+        // cross-lane steps) is formed only then.
+        bool any_lane = false;
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const bool grow = nb ? grow1 : grow0;
+        for (int nb = 0; nb < NB; ++nb) any_lane = any_lane || mx[nb] > m[nb] + 8.0f;
+        if (__any(any_lane)) {
+            float alpha[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                mx[nb] = fmaxf(mx[nb], __shfl_xor(mx[nb], 16));
+                mx[nb] = fmaxf(mx[nb], __shfl_xor(mx[nb], 32));
+                const bool grow = mx[nb] > m[nb] + 8.0f;
                 const float mn = grow ? mx[nb] : m[nb];
                 alpha[nb] = grow ? exp2_fast(m[nb] - mn) : 1.0f;
                 l[nb] *= alpha[nb];
@@ -246,10 +261,10 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 #pragma unroll
             for (int db = 0; db < DB; ++db)
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) acc[db][nb] *= alpha[nb];
+                for (int nb = 0; nb < NB; ++nb) acc[db][nb] *= alpha[nb];
         }
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
+        for (int nb = 0; nb < NB; ++nb) {
             const float mu = m[nb] == -INFINITY ? 0.0f : m[nb];
             float sum = 0.0f;
 #pragma unroll
@@ -267,9 +282,9 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         // ---- O^T += V^T P^T
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            bf16x8_t pb[2];
+            bf16x8_t pb[NB];
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
+            for (int nb = 0; nb < NB; ++nb) {
                 const f32x4_t& x0 = s[2 * kt][nb];
                 const f32x4_t& x1 = s[2 * kt + 1][nb];
                 uint4 u;
@@ -286,14 +301,14 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
                 const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
                 const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) acc[db][nb] = mfma16x16x32(a, pb[nb], acc[db][nb]);
+                for (int nb = 0; nb < NB; ++nb) acc[db][nb] = mfma16x16x32(a, pb[nb], acc[db][nb]);
             }
         }
     }
 
     if (!wave_has_rows) return;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
         float lt = l[nb];
         lt += __shfl_xor(lt, 16);
         lt += __shfl_xor(lt, 32);
@@ -317,10 +332,10 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged prefill: head_dim must be 128");
     if (p.S <= 0 || p.n_pages <= 0) return GENLLM_OK;
-    constexpr int WAVES = 4;
-    const int n_qt = (p.S + QW * WAVES - 1) / (QW * WAVES);
-    dim3 grid(n_qt, p.Hq);
-    hipLaunchKernelGGL((paged_prefill_kernel<128, WAVES>), grid, dim3(WAVES * 64), 0, stream, p);
+    constexpr int WAVES = 4, NB = kPrefillBlocks;
+    const int64_t n_qt = (p.S + 16 * NB * WAVES - 1) / (16 * NB * WAVES);
+    hipLaunchKernelGGL((paged_prefill_kernel<128, WAVES, NB>), dim3(unsigned(n_qt * p.Hq)), dim3(WAVES * 64), 0, stream,
+                       p);
     GENLLM_LAUNCH_CHECK("paged_prefill_kernel");
     return GENLLM_OK;
 }
