@@ -88,6 +88,11 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// s_waitcnt operand (gfx9 encoding) for "vmcnt(0)", leaving the LDS/scalar
+// and export counters unconstrained: vmcnt bits [3:0] and [15:14] = 0,
+// expcnt [6:4] = 7, lgkmcnt [11:8] = 15.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));  // MFMA A/B operand (8 bf16 per lane)
 typedef float f32x4_t __attribute__((ext_vector_type(4)));    // 16x16 MFMA C/D (4 fp32 per lane)
 

@@ -74,12 +74,15 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     bf16x8_t qb[NB][KS];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
+        // unconditional loads (row clamped into the chunk), zeroed after: a
+        // load under a branch keeps the compiler from proving it complete later
         const int s = q0 + 16 * nb + n16;
-        const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(s) * p.q_tok_stride;
+        const bool ok = s < p.S;
+        const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(ok ? s : p.S - 1) * p.q_tok_stride;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            uint4 u = make_uint4(0, 0, 0, 0);
-            if (s < p.S) u = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
+            uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
+            if (!ok) u = make_uint4(0, 0, 0, 0);
             qb[nb][ks] = as_bf16x8(u);
         }
     }
@@ -119,11 +122,14 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
     const uint16_t* kbase = p.k_pool + (tid >> 4) * p.kv_row + head_off + 8 * (tid & 15);
     const uint16_t* vbase = p.v_pool + ((2 * tp) % kPage) * p.kv_row + head_off + 8 * (tid >> 5);
-    const bool paged = p.k_ids != nullptr;
+    // kernel arguments used inside the lambdas, read once into registers
+    const int32_t* const k_ids = p.k_ids;
+    const int32_t* const v_ids = p.v_ids;
+    const bool paged = k_ids != nullptr;
     auto load_ids = [&](int tile) -> int {
         const int page = 4 * tile + (lane & 3);
         int id = 0;
-        if (lane < 8 && page * kPage < kv_end) id = !paged ? page : lane < 4 ? p.k_ids[page] : p.v_ids[page];
+        if (lane < 8 && page * kPage < kv_end) id = !paged ? page : lane < 4 ? k_ids[page] : v_ids[page];
         return id;
     };
     auto load_tile = [&](int tile, int ids) {
@@ -184,8 +190,13 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     };
 
     int ids_next = 0;
+    if (n_tiles > 0) load_tile(0, load_ids(0));
+    // Q and tile 0 have landed on every path.  Without this unconditional
+    // wait the compiler cannot prove that the Q loads completed before the
+    // loop and waits for all outstanding loads (the prefetched tiles too) at
+    // the first use of Q in every iteration.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     if (n_tiles > 0) {
-        load_tile(0, load_ids(0));
         store_tile(0);
         if (n_tiles > 1) load_tile(1, load_ids(1));
         if (n_tiles > 2) ids_next = load_ids(2);
