@@ -5,24 +5,27 @@
 // at q_abs = n_cached - S + s and attends keys 0..q_abs (causal, :164-181),
 // kv head = q head / groups (:158).
 //
-// Grid: query tiles x Hq workgroups of WAVES x 64 threads.  A workgroup owns
-// QW*WAVES consecutive queries of one q head; wave w owns QW = 16*NB of them
-// (NB 16-row MFMA blocks).  K/V tiles of 64 tokens (4 pages) are gathered through the
-// block table into LDS:
-//   K  as [token][dim]  (row pad 16 B),
-//   V  transposed as [dim][token] (row pad 8 B) -- pairs of tokens are packed
-//      into dwords so the transpose is plain ds_write_b32.
+// Grid: query tiles of 64 x Hq workgroups of 4 waves; wave w owns 16 queries
+// (one 16-row MFMA block).  Key tiles of 64 tokens (4 pages) are staged in LDS
+// double-buffered, K and V each as [token][dim] rows of 256 B whose 16-byte
+// chunks are XOR-swizzled (chunk c of row r at position c ^ (r % 16)), which
+// keeps both the K operand reads and the transposing V reads free of bank
+// conflicts.  Wave w moves page w of every tile, K and V, straight from HBM
+// into LDS with 16-byte LDS-direct loads (global_load_lds_dwordx4: lane i's
+// chunk lands at base + 16 i), so a tile costs no registers, no VALU and no
+// LDS store instructions.
 // Per tile and wave, with v_mfma_f32_16x16x32_bf16:
 //   S^T = K Q^T  (A = K from LDS: lane l -> token l%16 of a 16-block, dims
 //        32ks+8(l/16)..; B = Q^T held in registers).  D[tok][q] lands in lane
 //        q%16 + 16*(tok%16/4), register tok%4: every lane holds 16 keys of ONE
-//        query row per 16-query block, so the online softmax state (m, l) of a
-//        row is per lane and the row max needs only two cross-lane shuffles.
-//   O^T += V^T P^T  (A = V^T from LDS, two 8-byte reads; B = P^T taken from the
-//        lane's own S^T registers after exp2 and bf16 packing -- the 8 keys of
-//        lane group g for k-step kt are {32kt+4g+i, 32kt+16+4g+i}, i<4, and
-//        the V^T reads use the same 8 keys).  O^T[dim][q] again belongs to the
-//        lane's own query, so the rescale by 2^(m_old-m_new) is lane-local.
+//        query row, so the online softmax state (m, l) of a row is per lane.
+//   O^T += V^T P^T  (B = P^T from the lane's own S^T registers after exp2 and
+//        bf16 packing -- the 8 keys of lane group g for k-step kt are
+//        {32kt+4g+i, 32kt+16+4g+i}, i<4; A = V^T from two ds_read_b64_tr_b16
+//        of those two 4-key groups: in each 16-lane group, lane 4j+q points at
+//        V[key0+j][dim0+4q..+3] and lane i receives V[key0+0..3][dim0+i]).
+//        O^T[dim][q] again belongs to the lane's own query, so the rescale by
+//        2^(m_old-m_new) is lane-local.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -30,29 +33,40 @@ namespace genllm {
 
 namespace {
 
-constexpr int KT = 64;  // keys per tile (4 pages)
-// 16-row query blocks per wave: 1 keeps a wave at 184 registers, so two
-// workgroups (8 waves) share a CU and the grid's heavy/light pairing applies.
-constexpr int kPrefillBlocks = 1;
+constexpr int KT = 64;     // keys per tile (4 pages)
+constexpr int WAVES = 4;   // one page of each tile per wave
+constexpr int QW = 16;     // queries per wave
+constexpr int QT = QW * WAVES;
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
 
 __device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
     const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
     return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
-template <int D, int WAVES, int NB>
+__device__ __forceinline__ s16x4_t ds_read_tr(const lds_char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<__attribute__((address_space(3))) s16x4_t*>(const_cast<lds_char*>(p)));
+}
+
+template <int D>
 __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p) {
     static_assert(D == 128, "prefill kernel: head_dim 128");
-    constexpr int KS = D / 32;     // k-steps of the S^T product
-    constexpr int DB = D / 16;     // 16-dim blocks of O^T
-    constexpr int KROW = D + 8;    // K tile row stride (elements)
-    constexpr int VROW = KT + 4;   // V^T tile row stride (elements)
-    constexpr int NT = WAVES * 64;
-    constexpr int QW = 16 * NB;  // queries per wave: NB blocks of 16 rows
-    constexpr int QT = QW * WAVES;
+    constexpr int KS = D / 32;       // k-steps of the S^T product
+    constexpr int DB = D / 16;       // 16-dim blocks of O^T
+    constexpr int ROWB = D * 2;      // bytes per token row (16 chunks of 16 B)
+    constexpr int TILEB = KT * ROWB;  // bytes of a K (or V) tile
+    static_assert(ROWB == 16 * 16, "16 chunks per row: the swizzle is c ^ (r % 16)");
 
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * KT * KROW];  // two buffers
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * D * VROW];
+    // [buffer 0: K, V][buffer 1: K, V], separate arrays so that the compiler
+    // sees the tile being loaded and the tile being read as distinct memory
+    __shared__ __attribute__((aligned(16))) char lds_b0[2 * TILEB];
+    __shared__ __attribute__((aligned(16))) char lds_b1[2 * TILEB];
+    lds_char* const buf0 = (lds_char*)lds_b0;
+    lds_char* const buf1 = (lds_char*)lds_b1;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n16 = lane & 15, g = lane >> 4;
@@ -67,274 +81,222 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     const int heavy = (n_qt + 1) / 2;
     const int qt = rank < heavy ? n_qt - 1 - rank : rank - heavy;
     const int hkv = hq / p.G;
-    const int qabs0 = p.n_cached - p.S;   // absolute position of query 0
-    const int q0 = qt * QT + wv * QW;     // first query of this wave
+    const int qabs0 = p.n_cached - p.S;  // absolute position of query 0
+    const int q0 = qt * QT + wv * QW;    // first query of this wave
 
-    // Q^T operands (B): lane -> query q0 + 16nb + n16, dims 32ks + 8g..+7
-    bf16x8_t qb[NB][KS];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        // unconditional loads (row clamped into the chunk), zeroed after: a
-        // load under a branch keeps the compiler from proving it complete later
-        const int s = q0 + 16 * nb + n16;
+    // Q^T operand (B): lane -> query q0 + n16, dims 32ks + 8g..+7.  Loads are
+    // unconditional (row clamped), zeroed after.
+    bf16x8_t qb[KS];
+    {
+        const int s = q0 + n16;
         const bool ok = s < p.S;
         const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(ok ? s : p.S - 1) * p.q_tok_stride;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
             if (!ok) u = make_uint4(0, 0, 0, 0);
-            qb[nb][ks] = as_bf16x8(u);
+            qb[ks] = as_bf16x8(u);
         }
     }
 
-    float m[NB], l[NB];
+    float m = -INFINITY, l = 0.0f;
+    f32x4_t acc[DB];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) m[nb] = -INFINITY, l[nb] = 0.0f;
-    f32x4_t acc[DB][NB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[db][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int wg_last = min(qt * QT + QT, p.S) - 1;
     const int kv_end = p.causal ? min(qabs0 + wg_last + 1, p.n_cached) : p.n_cached;
     const int n_tiles = (kv_end + KT - 1) / KT;
     const bool wave_has_rows = q0 < p.S;
     const int w_last_abs = qabs0 + min(q0 + QW, p.S) - 1;
-    const int w_first_abs = qabs0 + q0;
 
-    // Pipeline (one barrier per tile, two LDS buffers):
-    //   iteration t: store tile t+1 (already in registers) into buffer (t+1)&1,
-    //   request tile t+2 from HBM into registers using its block-table entries
-    //   (fetched one iteration earlier), fetch the entries of tile t+3, then
-    //   compute tile t from buffer t&1.
-    // Thread -> data: K chunk e of a tile is token 16e + tid/16 (page e of the
-    // tile), dims 8*(tid%16)..+7; V task e is the token pair 2*(tid%32), +1
-    // (page (tid%32)/8), dims 8*(tid/32 + 8e)..+7.  Lanes 0..3 of every wave
-    // hold the tile's 4 K page ids, lanes 4..7 its 4 V page ids.
-    constexpr int KCH = KT * (D / 8) / NT;          // 16-byte K chunks per thread
-    constexpr int VTK = (KT / 2) * (D / 8) / NT;    // V token-pair tasks per thread
-    static_assert(KCH * NT == KT * (D / 8) && VTK * NT == (KT / 2) * (D / 8), "tile split");
-    static_assert(NT % (KT / 2) == 0 && (NT / (D / 8)) * KCH == KT && KCH == KT / kPage, "thread map");
-    uint4 kreg[KCH], va[VTK], vb[VTK];
-    // in-page element offsets are the same for every tile (tiles start on page boundaries)
-    const int tp = tid & (KT / 2 - 1);
-    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
-    const uint16_t* kbase = p.k_pool + (tid >> 4) * p.kv_row + head_off + 8 * (tid & 15);
-    const uint16_t* vbase = p.v_pool + ((2 * tp) % kPage) * p.kv_row + head_off + 8 * (tid >> 5);
-    // kernel arguments used inside the lambdas, read once into registers
+    // ---- tile staging.  Lanes 0..3 hold the K ids of the tile's 4 pages,
+    // lanes 4..7 the V ids; wave w loads page w.  Lane -> (row 4e + lane/16 of
+    // the page, chunk position lane%16) for instruction e = 0..3.
     const int32_t* const k_ids = p.k_ids;
     const int32_t* const v_ids = p.v_ids;
     const bool paged = k_ids != nullptr;
+    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
+    const uint16_t* const k_src = p.k_pool + head_off;
+    const uint16_t* const v_src = p.v_pool + head_off;
+    const int64_t kv_row = p.kv_row, page_elems = p.page_elems;
+    const int n_cached = p.n_cached;
     auto load_ids = [&](int tile) -> int {
         const int page = 4 * tile + (lane & 3);
         int id = 0;
         if (lane < 8 && page * kPage < kv_end) id = !paged ? page : lane < 4 ? k_ids[page] : v_ids[page];
         return id;
     };
-    auto load_tile = [&](int tile, int ids) {
-        const int tok0 = tile * KT;
-        const int64_t vid = __shfl(ids, 4 + (tp >> 3));
-        if (tok0 + KT <= p.n_cached) {  // whole tile cached: no per-load conditions
+    // Paged: page base = id * page_elems, rows 0..15.  Head-major tensor:
+    // page base = first token * kv_row, rows clamped to the last token
+    // (row - first token may go negative past the end; the absolute row
+    // stays n_cached - 1).
+    auto issue_tile = [&](int tile, int ids, lds_char* buf) {
+        const int tok_page = tile * KT + kPage * wv;  // first token of this wave's page
+        const int64_t kbase = paged ? int64_t(__builtin_amdgcn_readlane(ids, wv)) * page_elems : int64_t(tok_page) * kv_row;
+        const int64_t vbase = paged ? int64_t(__builtin_amdgcn_readlane(ids, 4 + wv)) * page_elems : kbase;
+        const int last = paged ? kPage - 1 : n_cached - 1 - tok_page;
+        const int dst0 = wv * (kPage * ROWB);
 #pragma unroll
-            for (int e = 0; e < KCH; ++e)
-                kreg[e] = *reinterpret_cast<const uint4*>(kbase + int64_t(__builtin_amdgcn_readlane(ids, e)) *
-                                                                      p.page_elems);
-#pragma unroll
-            for (int e = 0; e < VTK; ++e) {
-                const uint16_t* src = vbase + vid * p.page_elems + 8 * (NT / 32) * e;
-                va[e] = *reinterpret_cast<const uint4*>(src);
-                vb[e] = *reinterpret_cast<const uint4*>(src + p.kv_row);
-            }
-            return;
-        }
-#pragma unroll
-        for (int e = 0; e < KCH; ++e) {
-            const int pos = tok0 + 16 * e + (tid >> 4);
-            const int64_t id = __builtin_amdgcn_readlane(ids, e);
-            kreg[e] = make_uint4(0, 0, 0, 0);
-            if (pos < p.n_cached) kreg[e] = *reinterpret_cast<const uint4*>(kbase + id * p.page_elems);
-        }
-        const int pos = tok0 + 2 * tp;
-#pragma unroll
-        for (int e = 0; e < VTK; ++e) {
-            const uint16_t* src = vbase + vid * p.page_elems + 8 * (NT / 32) * e;
-            va[e] = make_uint4(0, 0, 0, 0);
-            vb[e] = make_uint4(0, 0, 0, 0);
-            if (pos < p.n_cached) va[e] = *reinterpret_cast<const uint4*>(src);
-            if (pos + 1 < p.n_cached) vb[e] = *reinterpret_cast<const uint4*>(src + p.kv_row);
+        for (int e = 0; e < 4; ++e) {
+            const int slot = 4 * e + (lane >> 4);
+            const int chunk = (lane & 15) ^ slot;  // row % 16 == slot: rows start on page boundaries
+            const int64_t roff = int64_t(min(slot, last)) * kv_row + 8 * chunk;
+            __builtin_amdgcn_global_load_lds(k_src + kbase + roff, buf + (dst0 + e * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(v_src + vbase + roff, buf + (TILEB + dst0 + e * 1024), 16, 0, 0);
         }
     };
-    auto store_tile = [&](int buf) {
-        uint16_t* kl = k_lds + buf * (KT * KROW);
-        uint16_t* vl = v_lds + buf * (D * VROW);
+    // V rows at or past kv_end of the tile hold no key (or one no query here
+    // may see); they are zeroed so that their zero probabilities never meet
+    // a non-finite value.  Each wave clears rows of its own page, after its
+    // own loads of them have landed.
+    auto clear_tail = [&](int tile, lds_char* buf) {
+        const int first = tile * KT + kPage * wv;
+        if (first + kPage <= kv_end) return;  // wave-uniform
 #pragma unroll
-        for (int e = 0; e < KCH; ++e) {
-            const int tt = 16 * e + (tid >> 4), ch = tid & 15;
-            *reinterpret_cast<uint4*>(&kl[tt * KROW + 8 * ch]) = kreg[e];
-        }
-        // V transposed: the dword at V^T[d][2tp] packs tokens 2tp (low) and 2tp+1 (high)
-#pragma unroll
-        for (int e = 0; e < VTK; ++e) {
-            const int ch = (tid >> 5) + (NT / 32) * e;
-            const uint32_t av[4] = {va[e].x, va[e].y, va[e].z, va[e].w};
-            const uint32_t bv[4] = {vb[e].x, vb[e].y, vb[e].z, vb[e].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                uint32_t* row0 = reinterpret_cast<uint32_t*>(&vl[(8 * ch + 2 * q) * VROW + 2 * tp]);
-                uint32_t* row1 = reinterpret_cast<uint32_t*>(&vl[(8 * ch + 2 * q + 1) * VROW + 2 * tp]);
-                *row0 = __builtin_amdgcn_perm(bv[q], av[q], 0x05040100u);  // low halves
-                *row1 = __builtin_amdgcn_perm(bv[q], av[q], 0x07060302u);  // high halves
-            }
+        for (int e = 0; e < 4; ++e) {
+            const int slot = 4 * e + (lane >> 4);  // the row lane's 16 bytes landed in: base + 16 lane
+            if (first + slot >= kv_end)
+                *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(
+                    buf + (TILEB + wv * (kPage * ROWB) + e * 1024 + 16 * lane)) = u32x4_t{0u, 0u, 0u, 0u};
         }
     };
 
-    int ids_next = 0;
-    if (n_tiles > 0) load_tile(0, load_ids(0));
-    // Q and tile 0 have landed on every path.  Without this unconditional
-    // wait the compiler cannot prove that the Q loads completed before the
-    // loop and waits for all outstanding loads (the prefetched tiles too) at
-    // the first use of Q in every iteration.
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    if (n_tiles > 0) {
-        store_tile(0);
-        if (n_tiles > 1) load_tile(1, load_ids(1));
-        if (n_tiles > 2) ids_next = load_ids(2);
-    }
-    for (int t = 0; t < n_tiles; ++t) {
+    // ---- one tile of attention from LDS (buf: K at 0, V at TILEB)
+    auto compute_tile = [&](int t, const lds_char* buf) {
         const int tok0 = t * KT;
-        __syncthreads();  // tile t is in LDS; nobody still reads buffer (t+1)&1
-        if (t + 1 < n_tiles) store_tile((t + 1) & 1);
-        if (t + 2 < n_tiles) {
-            load_tile(t + 2, ids_next);
-            if (t + 3 < n_tiles) ids_next = load_ids(t + 3);
-        }
-        if (!wave_has_rows || (p.causal && tok0 > w_last_abs)) continue;
-        const uint16_t* k_cur = k_lds + (t & 1) * (KT * KROW);
-        const uint16_t* v_cur = v_lds + (t & 1) * (D * VROW);
-
-        // ---- S^T = K Q^T
-        f32x4_t s[4][NB];
+        // S^T = K Q^T
+        f32x4_t s[4];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) s[mb][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int mb = 0; mb < 4; ++mb) s[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) {
-                const bf16x8_t a =
-                    as_bf16x8(*reinterpret_cast<const uint4*>(&k_cur[(16 * mb + n16) * KROW + 32 * ks + 8 * g]));
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) s[mb][nb] = mfma16x16x32(a, qb[nb][ks], s[mb][nb]);
+                const int row = 16 * mb + n16;
+                const int pos = (4 * ks + g) ^ n16;  // row % 16 == n16
+                const u32x4_t a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+                    buf + (row * ROWB + pos * 16));
+                s[mb] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[ks], s[mb]);
             }
 
-        // ---- online softmax, per lane = per query row
-        const bool need_mask = (p.causal && tok0 + KT - 1 > w_first_abs) || tok0 + KT > p.n_cached;
-        // Lazy rescale: a row's reference max m only moves (and its l, O^T are
-        // rescaled) when the tile max exceeds it by more than 2^8, so p <= 256.
-        // max over raw scores (scale >= 0), then p = exp2(s * scale*log2e - m), one fma
+        // online softmax, per lane = per query row
+        // A key is visible to this lane's query when kpos < lim (lim = n_cached,
+        // or q_abs + 1 when causal).  Keys of the tile as seen from this lane:
+        // tok0 + 16 mb + 4 g + i, so the test is (16 mb + i) < lim - tok0 - 4 g.
         const float c = p.scale_log2;
-        float mx[NB];
+        const int qpos = qabs0 + q0 + n16;
+        const int lim = p.causal ? min(qpos + 1, n_cached) : n_cached;
+        const int rel = lim - tok0 - 4 * g;
+        float mr = -INFINITY;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int qpos = qabs0 + q0 + 16 * nb + n16;
-            float mr = -INFINITY;
+        for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (need_mask) {
-                        const int kpos = tok0 + 16 * mb + 4 * g + i;
-                        if (kpos >= p.n_cached || (p.causal && kpos > qpos)) s[mb][nb][i] = -INFINITY;
-                    }
-                    mr = fmaxf(mr, s[mb][nb][i]);
-                }
-            mx[nb] = mr == -INFINITY ? -INFINITY : mr * c;  // this lane's 16 keys
-        }
-        // A lane's own keys decide whether any row may grow; the row max (two
-        // cross-lane steps) is formed only then.
-        bool any_lane = false;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) any_lane = any_lane || mx[nb] > m[nb] + 8.0f;
-        if (__any(any_lane)) {
-            float alpha[NB];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                mx[nb] = fmaxf(mx[nb], __shfl_xor(mx[nb], 16));
-                mx[nb] = fmaxf(mx[nb], __shfl_xor(mx[nb], 32));
-                const bool grow = mx[nb] > m[nb] + 8.0f;
-                const float mn = grow ? mx[nb] : m[nb];
-                alpha[nb] = grow ? exp2_fast(m[nb] - mn) : 1.0f;
-                l[nb] *= alpha[nb];
-                m[nb] = mn;
+            for (int i = 0; i < 4; ++i) {
+                s[mb][i] = (16 * mb + i < rel) ? s[mb][i] : -INFINITY;
+                mr = fmaxf(mr, s[mb][i]);
             }
+        // max over raw scores (scale >= 0), then p = exp2(s * scale*log2e - m), one fma.
+        // Lazy rescale: a row's reference max only moves (and its l, O^T are
+        // rescaled) when the tile max exceeds it by more than 2^8, so p <= 256;
+        // a lane's own 16 keys decide whether any row may grow, and the row max
+        // (two cross-lane steps) is formed only then.
+        float mx = mr == -INFINITY ? -INFINITY : mr * c;
+        if (__any(mx > m + 8.0f)) {
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool grow = mx > m + 8.0f;
+            const float mn = grow ? mx : m;
+            const float alpha = grow ? exp2_fast(m - mn) : 1.0f;
+            l *= alpha;
+            m = mn;
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) acc[db][nb] *= alpha[nb];
+            for (int db = 0; db < DB; ++db) acc[db] *= alpha;
         }
+        const float mu = m == -INFINITY ? 0.0f : m;
+        float sum = 0.0f;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const float mu = m[nb] == -INFINITY ? 0.0f : m[nb];
-            float sum = 0.0f;
+        for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float e = exp2_fast(__builtin_fmaf(s[mb][nb][i], c, -mu));
-                    if (need_mask && s[mb][nb][i] == -INFINITY) e = 0.0f;  // also when scale == 0
-                    s[mb][nb][i] = e;
-                    sum += e;
-                }
-            l[nb] += sum;
-        }
+            for (int i = 0; i < 4; ++i) {
+                // masked keys give exactly 0, also when scale == 0
+                const float e = (16 * mb + i < rel) ? exp2_fast(__builtin_fmaf(s[mb][i], c, -mu)) : 0.0f;
+                s[mb][i] = e;
+                sum += e;
+            }
+        l += sum;
 
-        // ---- O^T += V^T P^T
+        // O^T += V^T P^T
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            bf16x8_t pb[NB];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const f32x4_t& x0 = s[2 * kt][nb];
-                const f32x4_t& x1 = s[2 * kt + 1][nb];
-                uint4 u;
-                u.x = bf16_pair_rne(x0[0], x0[1]);
-                u.y = bf16_pair_rne(x0[2], x0[3]);
-                u.z = bf16_pair_rne(x1[0], x1[1]);
-                u.w = bf16_pair_rne(x1[2], x1[3]);
-                pb[nb] = as_bf16x8(u);
-            }
+            uint4 u;
+            u.x = bf16_pair_rne(s[2 * kt][0], s[2 * kt][1]);
+            u.y = bf16_pair_rne(s[2 * kt][2], s[2 * kt][3]);
+            u.z = bf16_pair_rne(s[2 * kt + 1][0], s[2 * kt + 1][1]);
+            u.w = bf16_pair_rne(s[2 * kt + 1][2], s[2 * kt + 1][3]);
+            const bf16x8_t pb = as_bf16x8(u);
+            // this lane's source address for the transposing reads: row
+            // key0 + n16/4, dims 16db + 4(n16%4)..+3 (chunk 2db + (n16%4)/2, half n16%2)
+            // The byte offsets are formed as one integer and applied to the
+            // buffer in a single step: the compiler attributes an LDS access
+            // to its array (and so can tell it apart from the loads still
+            // streaming into the other buffer, without waiting for them) only
+            // through a short chain of pointer arithmetic.
+            const int row0 = 32 * kt + 4 * g + (n16 >> 2), row1 = row0 + 16;
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const uint16_t* vr = &v_cur[(16 * db + n16) * VROW + 32 * kt + 4 * g];
-                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-                const bf16x8_t a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) acc[db][nb] = mfma16x16x32(a, pb[nb], acc[db][nb]);
+                const int chunk = 2 * db + ((n16 & 3) >> 1), half = (n16 & 1) * 8;
+                const int off0 = TILEB + row0 * ROWB + ((chunk ^ (row0 & 15)) * 16) + half;
+                const int off1 = TILEB + row1 * ROWB + ((chunk ^ (row1 & 15)) * 16) + half;
+                const s16x4_t lo = ds_read_tr(buf + off0);
+                const s16x4_t hi = ds_read_tr(buf + off1);
+                const s16x4_t a8[2] = {lo, hi};
+                acc[db] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a8), pb, acc[db]);
             }
         }
+    };
+
+    // ---- pipeline: one barrier per tile, two LDS buffers.  Iteration t waits
+    // for its own loads of tile t, clears the tail, meets the other waves (tile
+    // t complete in LDS; everybody done reading tile t-1), starts tile t+1 into
+    // the other buffer, fetches the ids of tile t+2, then computes tile t.
+    int ids_next = 0;
+    if (n_tiles > 0) {
+        const int ids0 = load_ids(0);
+        if (n_tiles > 1) ids_next = load_ids(1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // q and ids landed on every path
+        issue_tile(0, ids0, buf0);
+    }
+    auto step = [&](int t, lds_char* cur, lds_char* nxt) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        clear_tail(t, cur);
+        __syncthreads();
+        if (t + 1 < n_tiles) {
+            issue_tile(t + 1, ids_next, nxt);
+            if (t + 2 < n_tiles) ids_next = load_ids(t + 2);
+        }
+        if (wave_has_rows && !(p.causal && t * KT > w_last_abs)) compute_tile(t, cur);
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        step(t, buf0, buf1);
+        if (t + 1 < n_tiles) step(t + 1, buf1, buf0);
     }
 
     if (!wave_has_rows) return;
+    float lt = l;
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const float inv = 1.0f / lt;
+    const int s = q0 + n16;
+    if (s >= p.S) return;
+    uint16_t* orow = p.out + int64_t(hq) * p.o_head_stride + int64_t(s) * p.o_tok_stride;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        float lt = l[nb];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
-        const float inv = 1.0f / lt;
-        const int s = q0 + 16 * nb + n16;
-        if (s >= p.S) continue;
-        uint16_t* orow = p.out + int64_t(hq) * p.o_head_stride + int64_t(s) * p.o_tok_stride;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            const f32x4_t& a = acc[db][nb];
-            uint2 w;
-            w.x = pack2(f32_to_bf16_ref(a[0] * inv), f32_to_bf16_ref(a[1] * inv));
-            w.y = pack2(f32_to_bf16_ref(a[2] * inv), f32_to_bf16_ref(a[3] * inv));
-            *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = w;
-        }
+    for (int db = 0; db < DB; ++db) {
+        const f32x4_t& a = acc[db];
+        uint2 w;
+        w.x = pack2(f32_to_bf16_ref(a[0] * inv), f32_to_bf16_ref(a[1] * inv));
+        w.y = pack2(f32_to_bf16_ref(a[2] * inv), f32_to_bf16_ref(a[3] * inv));
+        *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = w;
     }
 }
 
@@ -343,10 +305,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged prefill: head_dim must be 128");
     if (p.S <= 0 || p.n_pages <= 0) return GENLLM_OK;
-    constexpr int WAVES = 4, NB = kPrefillBlocks;
-    const int64_t n_qt = (p.S + 16 * NB * WAVES - 1) / (16 * NB * WAVES);
-    hipLaunchKernelGGL((paged_prefill_kernel<128, WAVES, NB>), dim3(unsigned(n_qt * p.Hq)), dim3(WAVES * 64), 0, stream,
-                       p);
+    const int64_t n_qt = (p.S + QT - 1) / QT;
+    hipLaunchKernelGGL(paged_prefill_kernel<128>, dim3(unsigned(n_qt * p.Hq)), dim3(WAVES * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_prefill_kernel");
     return GENLLM_OK;
 }
