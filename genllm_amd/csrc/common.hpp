@@ -93,6 +93,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 // expcnt [6:4] = 7, lgkmcnt [11:8] = 15.
 constexpr int kWaitVmcnt0 = 0x0F70;
 
+// Buffer resource word 3 for raw (untyped) buffer accesses on gfx9-family
+// GPUs: 32-bit data format, no swizzle, no index addressing.  Loads at or
+// past the resource's size return zeros.
+constexpr int kBufferFlags = 0x00020000;
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));  // MFMA A/B operand (8 bf16 per lane)
 typedef float f32x4_t __attribute__((ext_vector_type(4)));    // 16x16 MFMA C/D (4 fp32 per lane)
 

@@ -52,10 +52,6 @@ constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 element
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
-// Buffer resource word 3 for raw (untyped) buffer accesses on gfx9-family
-// GPUs: 32-bit data format, no swizzle, no index addressing.
-constexpr int kBufferFlags = 0x00020000;
-
 __device__ __forceinline__ f32x4_t mfma16x16x16(const s16x4_t& a, const s16x4_t& b, const f32x4_t& c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }

@@ -8,12 +8,14 @@
 // Grid: query tiles of 64 x Hq workgroups of 4 waves; wave w owns 16 queries
 // (one 16-row MFMA block).  Key tiles of 64 tokens (4 pages) are staged in LDS
 // double-buffered, K and V each as [token][dim] rows of 256 B whose 16-byte
-// chunks are XOR-swizzled (chunk c of row r at position c ^ (r % 16)), which
-// keeps both the K operand reads and the transposing V reads free of bank
-// conflicts.  Wave w moves page w of every tile, K and V, straight from HBM
-// into LDS with 16-byte LDS-direct loads (global_load_lds_dwordx4: lane i's
-// chunk lands at base + 16 i), so a tile costs no registers, no VALU and no
-// LDS store instructions.
+// chunks are XOR-swizzled (chunk c of row r at position c ^ swz(r % 16), with
+// swz(r) = 2 (r % 8) + r / 8), which keeps both the K operand reads and the
+// transposing V reads free of LDS bank conflicts.  Wave w moves page w of
+// every tile, K and V, straight from HBM into LDS with 16-byte buffer loads in
+// LDS mode (lane i's 16 bytes land at base + 16 i), so a tile costs no
+// registers, no VALU and no LDS store instructions; one buffer resource per
+// page (base = the page of this kv head, size = the bytes its 16 rows span)
+// bounds every load.
 // Per tile and wave, with v_mfma_f32_16x16x32_bf16:
 //   S^T = K Q^T  (A = K from LDS: lane l -> token l%16 of a 16-block, dims
 //        32ks+8(l/16)..; B = Q^T held in registers).  D[tok][q] lands in lane
@@ -26,6 +28,8 @@
 //        V[key0+j][dim0+4q..+3] and lane i receives V[key0+0..3][dim0+i]).
 //        O^T[dim][q] again belongs to the lane's own query, so the rescale by
 //        2^(m_old-m_new) is lane-local.
+// Causal masking is applied only to the tiles that reach past the first
+// query of the wave (the diagonal) or past the cache end.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -40,12 +44,18 @@ constexpr int QT = QW * WAVES;
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) char lds_char;
 
+// two fp32 -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
-    const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
-    return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
+
+// chunk-position swizzle of a 256-byte LDS row: bijective on r % 16, and
+// 2 (r % 8) separates the 32-byte chunk pairs of eight consecutive rows
+__device__ __forceinline__ constexpr int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
 __device__ __forceinline__ s16x4_t ds_read_tr(const lds_char* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -68,7 +78,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     lds_char* const buf0 = (lds_char*)lds_b0;
     lds_char* const buf1 = (lds_char*)lds_b1;
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS bases go to scalar registers
     const int n16 = lane & 15, g = lane >> 4;
     // Grid order pairs heavy and light causal tiles: the first half of the
     // workgroups takes query tiles from the last (most keys) downwards, the
@@ -109,6 +120,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     const int n_tiles = (kv_end + KT - 1) / KT;
     const bool wave_has_rows = q0 < p.S;
     const int w_last_abs = qabs0 + min(q0 + QW, p.S) - 1;
+    // keys below wave_lim are visible to every query of the wave
+    const int wave_lim = p.causal ? min(qabs0 + q0 + 1, p.n_cached) : p.n_cached;
 
     // ---- tile staging.  Lanes 0..3 hold the K ids of the tile's 4 pages,
     // lanes 4..7 the V ids; wave w loads page w.  Lane -> (row 4e + lane/16 of
@@ -127,23 +140,45 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         if (lane < 8 && page * kPage < kv_end) id = !paged ? page : lane < 4 ? k_ids[page] : v_ids[page];
         return id;
     };
-    // Paged: page base = id * page_elems, rows 0..15.  Head-major tensor:
-    // page base = first token * kv_row, rows clamped to the last token
-    // (row - first token may go negative past the end; the absolute row
-    // stays n_cached - 1).
+    // Lane byte offsets inside a page, the same for every tile: instruction e
+    // fills rows 4e..4e+3, lane -> row 4e + lane/16 (rows start on page
+    // boundaries, so row % 16 is that slot), position lane%16 <- chunk
+    // (lane%16) ^ swz(slot).
+    const int kv_row_bytes = int(kv_row) * 2;
+    uint32_t dma_off[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int slot = 4 * e + (lane >> 4);
+        dma_off[e] = uint32_t(slot * kv_row_bytes + 16 * ((lane & 15) ^ swz(slot)));
+    }
+    // Paged: the page of id k starts at k * page_elems; its 16 rows of this kv
+    // head span 15 kv_row + D elements.  Head-major tensor: the "page" starts
+    // at its first token and holds the rows still below n_cached -- the buffer
+    // returns zeros past them.
+    const uint32_t page_span = uint32_t(15 * kv_row_bytes + ROWB);
     auto issue_tile = [&](int tile, int ids, lds_char* buf) {
         const int tok_page = tile * KT + kPage * wv;  // first token of this wave's page
-        const int64_t kbase = paged ? int64_t(__builtin_amdgcn_readlane(ids, wv)) * page_elems : int64_t(tok_page) * kv_row;
-        const int64_t vbase = paged ? int64_t(__builtin_amdgcn_readlane(ids, 4 + wv)) * page_elems : kbase;
-        const int last = paged ? kPage - 1 : n_cached - 1 - tok_page;
+        int64_t kbase, vbase;
+        uint32_t span;
+        if (paged) {
+            kbase = int64_t(__builtin_amdgcn_readlane(ids, wv)) * page_elems;
+            vbase = int64_t(__builtin_amdgcn_readlane(ids, 4 + wv)) * page_elems;
+            span = page_span;
+        } else {
+            kbase = vbase = int64_t(tok_page) * kv_row;
+            // (readfirstlane: the value is uniform, keep it in a scalar register
+            // so the buffer resource needs no per-lane loop)
+            span = uint32_t(__builtin_amdgcn_readfirstlane(max(min(n_cached - tok_page, kPage), 0) * kv_row_bytes));
+        }
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)(k_src + kbase), 0, span, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)(v_src + vbase), 0, span, kBufferFlags);
         const int dst0 = wv * (kPage * ROWB);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int slot = 4 * e + (lane >> 4);
-            const int chunk = (lane & 15) ^ slot;  // row % 16 == slot: rows start on page boundaries
-            const int64_t roff = int64_t(min(slot, last)) * kv_row + 8 * chunk;
-            __builtin_amdgcn_global_load_lds(k_src + kbase + roff, buf + (dst0 + e * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(v_src + vbase + roff, buf + (TILEB + dst0 + e * 1024), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (__attribute__((address_space(3))) void*)(buf + (dst0 + e * 1024)),
+                                                     16, dma_off[e], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (__attribute__((address_space(3))) void*)(buf + (TILEB + dst0 + e * 1024)),
+                                                     16, dma_off[e], 0, 0, 0);
         }
     };
     // V rows at or past kv_end of the tile hold no key (or one no query here
@@ -162,8 +197,9 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         }
     };
 
-    // ---- one tile of attention from LDS (buf: K at 0, V at TILEB)
-    auto compute_tile = [&](int t, const lds_char* buf) {
+    // ---- one tile of attention from LDS (buf: K at 0, V at TILEB).  masked:
+    // the tile reaches past the first query of the wave or past the cache end.
+    auto compute_tile = [&](int t, const lds_char* buf, bool masked) {
         const int tok0 = t * KT;
         // S^T = K Q^T
         f32x4_t s[4];
@@ -174,7 +210,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) {
                 const int row = 16 * mb + n16;
-                const int pos = (4 * ks + g) ^ n16;  // row % 16 == n16
+                const int pos = (4 * ks + g) ^ swz(n16);  // row % 16 == n16
                 const u32x4_t a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
                     buf + (row * ROWB + pos * 16));
                 s[mb] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[ks], s[mb]);
@@ -184,24 +220,33 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         // A key is visible to this lane's query when kpos < lim (lim = n_cached,
         // or q_abs + 1 when causal).  Keys of the tile as seen from this lane:
         // tok0 + 16 mb + 4 g + i, so the test is (16 mb + i) < lim - tok0 - 4 g.
-        const float c = p.scale_log2;
-        const int qpos = qabs0 + q0 + n16;
-        const int lim = p.causal ? min(qpos + 1, n_cached) : n_cached;
-        const int rel = lim - tok0 - 4 * g;
+        // The scale (>= 0, checked by the host) is raised to at least FLT_MIN,
+        // so that a masked score of -inf gives exp2(-inf * c - m) = 0 without a
+        // select; at scale 0 every weight stays exp2(~0) = 1.
+        const float c = fmaxf(p.scale_log2, __FLT_MIN__);
+        if (masked) {
+            // wave-uniform; the empty asm keeps this a branch of its own
+            // instead of selects on every tile
+            __asm__ volatile("");
+            const int qpos = qabs0 + q0 + n16;
+            const int lim = p.causal ? min(qpos + 1, n_cached) : n_cached;
+            const int rel = lim - tok0 - 4 * g;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[mb][i] = (16 * mb + i < rel) ? s[mb][i] : -INFINITY;
+        }
         float mr = -INFINITY;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s[mb][i] = (16 * mb + i < rel) ? s[mb][i] : -INFINITY;
-                mr = fmaxf(mr, s[mb][i]);
-            }
-        // max over raw scores (scale >= 0), then p = exp2(s * scale*log2e - m), one fma.
+            for (int i = 0; i < 4; ++i) mr = fmaxf(mr, s[mb][i]);
+        // max over raw scores (c > 0), then p = exp2(s * scale*log2e - m), one fma.
         // Lazy rescale: a row's reference max only moves (and its l, O^T are
         // rescaled) when the tile max exceeds it by more than 2^8, so p <= 256;
         // a lane's own 16 keys decide whether any row may grow, and the row max
         // (two cross-lane steps) is formed only then.
-        float mx = mr == -INFINITY ? -INFINITY : mr * c;
+        float mx = mr * c;
         if (__any(mx > m + 8.0f)) {
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -219,8 +264,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                // masked keys give exactly 0, also when scale == 0
-                const float e = (16 * mb + i < rel) ? exp2_fast(__builtin_fmaf(s[mb][i], c, -mu)) : 0.0f;
+                const float e = exp2_fast(__builtin_fmaf(s[mb][i], c, -mu));  // masked: exactly 0
                 s[mb][i] = e;
                 sum += e;
             }
@@ -246,8 +290,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 const int chunk = 2 * db + ((n16 & 3) >> 1), half = (n16 & 1) * 8;
-                const int off0 = TILEB + row0 * ROWB + ((chunk ^ (row0 & 15)) * 16) + half;
-                const int off1 = TILEB + row1 * ROWB + ((chunk ^ (row1 & 15)) * 16) + half;
+                const int off0 = TILEB + row0 * ROWB + ((chunk ^ swz(row0 & 15)) * 16) + half;
+                const int off1 = TILEB + row1 * ROWB + ((chunk ^ swz(row1 & 15)) * 16) + half;
                 const s16x4_t lo = ds_read_tr(buf + off0);
                 const s16x4_t hi = ds_read_tr(buf + off1);
                 const s16x4_t a8[2] = {lo, hi};
@@ -275,7 +319,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
             issue_tile(t + 1, ids_next, nxt);
             if (t + 2 < n_tiles) ids_next = load_ids(t + 2);
         }
-        if (wave_has_rows && !(p.causal && t * KT > w_last_abs)) compute_tile(t, cur);
+        // masked unless every key of the tile is visible to every query of the wave
+        if (wave_has_rows && !(p.causal && t * KT > w_last_abs)) compute_tile(t, cur, t * KT + KT > wave_lim);
     };
     for (int t = 0; t < n_tiles; t += 2) {
         step(t, buf0, buf1);
