@@ -270,11 +270,19 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
                                1.0 / np.sqrt(D), ws)
 
     avg_us, _ = time_launches(torch, all_layers, iters, warm=2)
+    # the same 36-layer sequence captured once into a HIP graph and replayed
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        all_layers(0)
+    g_us, _ = time_launches(torch, lambda i: graph.replay(), iters, warm=2)
+    del graph
     m5.close()
     b5 = layers * decode_kernel_bytes(N)
     gbs = b5 / (avg_us * 1e-6) / 1e9
     return {"total_us": round(avg_us, 2), "us_per_layer": round(avg_us / layers, 3), "bytes": b5,
-            "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+            "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "graph_total_us": round(g_us, 2), "graph_us_per_layer": round(g_us / layers, 3),
+            "graph_GB_s": round(b5 / (g_us * 1e-6) / 1e9, 1)}
 
 
 def copy_calibration(np, torch, paged, synth, call, mib=256, iters=20):

@@ -45,7 +45,8 @@ namespace genllm {
 
 namespace {
 constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;       // waves of a split workgroup
+constexpr int kMergeWaves = 4;  // waves of a merge workgroup
 constexpr int kMaxSplits = 256;
 constexpr int PF = 3;          // pages in flight per wave (3: two waves per SIMD fit)
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
@@ -67,7 +68,7 @@ struct PageRegs {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
+__global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p) {
     static_assert(D == 128, "decode kernel: head_dim 128");
     constexpr int KS = D / 32;  // S^T k-steps
     constexpr int DB = D / 16;  // O^T dim blocks
@@ -342,10 +343,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(AttnParams p) {
 // to 64 splits); the 4 partials then meet in LDS with the same rule
 //   M = max M_w, L = sum L_w 2^(M_w - M), O = sum O_w 2^(M_w - M), out = O / L.
 template <int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
+__global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_merge_kernel(AttnParams p) {
     constexpr int U = 16;  // splits in flight per lane
-    __shared__ float s_o[kWaves][D];
-    __shared__ float s_m[kWaves], s_l[kWaves];
+    __shared__ float s_o[kMergeWaves][D];
+    __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ri = blockIdx.x, h = blockIdx.y;
     const int rows = p.G * p.S;
@@ -357,11 +358,11 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
     const int64_t sstride = int64_t(rows) * D / 2;  // float2 units between splits
 
     float mw = -INFINITY, lw = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (int s0 = wv; s0 < ns; s0 += kWaves * U) {
+    for (int s0 = wv; s0 < ns; s0 += kMergeWaves * U) {
         float2 ov[U], mv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int s2 = s0 + kWaves * u;
+            const int s2 = s0 + kMergeWaves * u;
             ov[u] = s2 < ns ? po[s2 * sstride] : make_float2(0.0f, 0.0f);
             mv[u] = s2 < ns ? ml[s2 * rows] : make_float2(-INFINITY, 0.0f);
         }
@@ -392,10 +393,10 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(AttnParams p) {
     if (wv == 0) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, s_m[w2]);
+        for (int w2 = 0; w2 < kMergeWaves; ++w2) M = fmaxf(M, s_m[w2]);
         float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
+        for (int w2 = 0; w2 < kMergeWaves; ++w2) {
             const float e = s_m[w2] == -INFINITY ? 0.0f : exp2_fast(s_m[w2] - M);
             L += s_l[w2] * e;
             O0 += s_o[w2][d2] * e;
@@ -450,10 +451,10 @@ int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (p.n_pages <= 0) return GENLLM_OK;
     if (p.n_splits > kMaxSplits || p.pages_per_split > 64 * kWaves || p.G * p.S > kRows)
         return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
-    hipLaunchKernelGGL(paged_decode_kernel<128>, dim3(p.n_splits, p.Hkv), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(paged_decode_kernel<128>, dim3(p.n_splits, p.Hkv), dim3(kWaves * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1) {
-        hipLaunchKernelGGL(paged_decode_merge_kernel<128>, dim3(p.G * p.S, p.Hkv), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(paged_decode_merge_kernel<128>, dim3(p.G * p.S, p.Hkv), dim3(kMergeWaves * 64), 0, stream, p);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;
