@@ -14,11 +14,13 @@ dominant kernel (paged_decode_kernel + its split merge) timed alone with HIP
 events around each launch on the launch stream, against 8 TB/s; its HBM
 traffic comes from the committed rocprofv3 --pmc summary when present.
 Secondary figures (same line): config 2 fused append GB/s, config 4 causal
-prefill TFLOPS, config 5 36-layer long-context decode.  cpu_baseline = the
-oracle (single thread) on a bounded sample of the headline workload.
+prefill TFLOPS, config 5 36-layer long-context decode (eager and replayed as
+one HIP graph), and the Qwen3-4B fused Q/K/V projection feeding the path (decode
+GEMV GB/s, 2048-token GEMM TFLOPS).  cpu_baseline = the oracle (single
+thread) on a bounded sample of the headline workload.
 
---only {headline,append,prefill,longctx} runs one workload alone (for
-rocprofv3 passes); the line then carries only that workload's figures.
+--only {headline,append,prefill,longctx,linear,copy} runs one workload alone
+(for rocprofv3 passes); the line then carries only that workload's figures.
 """
 from __future__ import annotations
 
@@ -46,7 +48,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
-    ap.add_argument("--only", choices=["headline", "append", "prefill", "longctx", "copy"], default=None)
+    ap.add_argument("--only", choices=["headline", "append", "prefill", "longctx", "linear", "copy"], default=None)
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -285,6 +287,35 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
             "graph_GB_s": round(b5 / (g_us * 1e-6) / 1e9, 1)}
 
 
+def linear_qkv(np, torch, paged, synth, call, iters=40):
+    """Qwen3-4B fused Q/K/V projection (hidden 2560 -> (32 + 2*8) * 128 = 6144,
+    Qwen3.cpp:130-134) through genllm_linear: one decode token (the
+    order-exact GEMV, HBM-bound on the 31.5 MB of weights; 16 weight copies
+    rotate so the MALL cannot serve them) and a 2048-token prefill chunk
+    (rocBLAS GEMM + epilogue)."""
+    K, N, copies = 2560, 6144, 16
+    ws_ = [torch.empty((N, K), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
+    for c, w in enumerate(ws_):
+        paged.fill_normal_bf16(w, 900 + c)
+    x1 = torch.empty((1, K), dtype=torch.bfloat16, device="cuda")
+    paged.fill_normal_bf16(x1, 7)
+    o1 = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+    gemv_us, _ = time_launches(torch, lambda i: paged.linear(x1, ws_[i % copies], o1), iters)
+    gemv_bytes = N * K * 2 + K * 2 + N * 2
+    M = 2048
+    xm = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
+    paged.fill_normal_bf16(xm, 8)
+    om = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    wsp = torch.empty(paged.linear_workspace_bytes(M, K, N), dtype=torch.uint8, device="cuda")
+    gemm_us, _ = time_launches(torch, lambda i: paged.linear(xm, ws_[i % copies], om, workspace=wsp), iters // 4)
+    gemm_flops = 2 * M * K * N
+    return {"gemv_rows": 1, "gemv_avg_launch_us": round(gemv_us, 3), "gemv_bytes": gemv_bytes,
+            "gemv_GB_s": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
+            "gemv_frac_hbm": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "gemm_rows": M, "gemm_avg_launch_us": round(gemm_us, 2),
+            "gemm_TFLOPS": round(gemm_flops / (gemm_us * 1e-6) / 1e12, 1)}
+
+
 def copy_calibration(np, torch, paged, synth, call, mib=256, iters=20):
     """A plain device copy of known size (torch copy_), the reference point that
     scales the FETCH_SIZE / WRITE_SIZE counters of the rocprofv3 --pmc passes."""
@@ -359,7 +390,7 @@ def main():
     common = (np, torch, paged, synth, call)
     if args.only and args.only != "headline":
         fn = {"append": append_cfg2, "prefill": prefill_cfg4, "longctx": longctx_cfg5,
-              "copy": copy_calibration}[args.only]
+              "linear": linear_qkv, "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, **fn(*common)}), flush=True)
         return
 
@@ -384,7 +415,7 @@ def main():
     }
     if not args.skip_secondary and not args.only:
         result["secondary"] = {"append_config2": append_cfg2(*common), "prefill_config4": prefill_cfg4(*common),
-                               "longctx_config5": longctx_cfg5(*common)}
+                               "longctx_config5": longctx_cfg5(*common), "linear_qkv_4b": linear_qkv(*common)}
     if not args.skip_cpu and not args.only:
         result["cpu_baseline"] = cpu_baseline(mgr, np, paged, synth, args, seed)
     mgr.close()

@@ -95,6 +95,8 @@ SIGNATURES = {
     "genllm_paged_prefill": (_int, [_P, _i64, _i64, _P, _i64, _i64, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32,
                                     _i32, _f, _i32, _P]),
     "genllm_flash_attention": (_int, [_P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, _i32, _P]),
+    "genllm_linear_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "genllm_linear": (_int, [_P, _P, _P, _P, _i64, _i64, _i64, _P, _sz, _P]),
     "genllm_fill_normal_bf16": (_int, [_P, _sz, _u64, _u64, _P]),
     "genllm_selftest_mfma": (_int, [_i32, _P, _P, _P, _P]),
 }

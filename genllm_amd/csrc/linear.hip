@@ -1,0 +1,264 @@
+// linear.hip -- bf16 linear layer: LinearImpl (src/backend/cpu/linear.cpp:46-122,
+// :325-345; src/backend/cuda/linear.cu:72-126) for the Q/K/V projections that
+// feed the paged attention op (Qwen3.cpp:130-134):
+//   out[r][c] = bf16( sum_k x[r][k] * w[c][k] + bias[c] )
+// x [rows][common], w [cols][common] (transpose_w = 1), bias [cols] or null,
+// fp32 accumulation, one rounding (the bfloat16_t constructor's rules).
+//
+// rows <= kGemvRows (a decode step): linear_gemv_kernel, HBM-bound on the
+// weights, reproduces the CPU reference's summation order exactly, so the
+// result is bit-identical to it.  The reference sums each output over K-blocks
+// of 256 elements: inside a block two 8-lane accumulators (sum0 takes elements
+// 16i+l, sum1 elements 16i+8+l, one fused multiply-add each, i ascending), then
+// v = sum0 + sum1 lane-wise and the block adds (t0+t1)+(t2+t3), t[i] =
+// v[i]+v[i+4], to the running fp32 sum; a trailing 8-element group adds the
+// same tree of its rounded products.  Here one GPU lane carries the 8 lanes
+// of one accumulator of one block (16-byte weight loads, 8 fused
+// multiply-adds each), its partner lane the other accumulator; the pair forms
+// the block's tree value, and one lane per output adds the blocks in order.
+// (A product of two bf16 values is exact in fp32, so the fused and unfused
+// forms of the 8-element group agree.)
+//
+// More rows: rocBLAS gemm_ex (bf16 inputs, fp32 compute, fp32 result in the
+// caller's workspace), then linear_epilogue_kernel adds the bias in fp32 and
+// rounds once; the summation order is rocBLAS's, so results match the
+// reference within fp32 accumulation error, not bit for bit.
+#include <rocblas/rocblas.h>
+
+#include <map>
+#include <mutex>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace genllm {
+
+namespace {
+
+constexpr int kGemvRows = 4;     // rows handled by the order-exact kernel
+constexpr int kBlockK = 256;     // the reference's K blocking (KR)
+constexpr int kGemvThreads = 256;
+
+__device__ __forceinline__ void bf16x8_to_f32(const uint4& u, float f[8]) {
+    f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x);
+    f[2] = bf16_lo(u.y); f[3] = bf16_hi(u.y);
+    f[4] = bf16_lo(u.z); f[5] = bf16_hi(u.z);
+    f[6] = bf16_lo(u.w); f[7] = bf16_hi(u.w);
+}
+
+__device__ __forceinline__ float tree8(const float v[8]) {
+    const float t0 = v[0] + v[4], t1 = v[1] + v[5], t2 = v[2] + v[6], t3 = v[3] + v[7];
+    return (t0 + t1) + (t2 + t3);
+}
+
+// Work item = (output column c, K-block b, accumulator h); adjacent lanes hold
+// the two accumulators of one block.  Items of a workgroup cover whole columns
+// (cols_per_wg = 256 / (2 nb)), so the block values of a column meet in LDS.
+template <int R>
+__global__ __launch_bounds__(kGemvThreads) void linear_gemv_kernel(const uint16_t* __restrict__ x,
+                                                                   const uint16_t* __restrict__ w,
+                                                                   const uint16_t* __restrict__ bias,
+                                                                   uint16_t* __restrict__ out, int common, int cols,
+                                                                   int nb, int cols_per_wg) {
+    __shared__ float s_h1[R][kGemvThreads / 2], s_h2[R][kGemvThreads / 2];
+    const int t = threadIdx.x;
+    const int pair = t >> 1, h = t & 1;
+    const int col0 = int(blockIdx.x) * cols_per_wg;
+    const int lc = pair / nb, b = pair - lc * nb;  // column within the workgroup, block
+    const int c = col0 + lc;
+    const bool item = lc < cols_per_wg && c < cols;
+    const int k0 = b * kBlockK;
+    const int k_len = min(kBlockK, common - k0);
+    const int n16 = k_len >> 4;               // 16-element steps of the block
+    const bool rem8 = (k_len - 16 * n16) >= 8;  // a trailing 8-element group (common % 8 == 0)
+
+    float s[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) s[r][l] = 0.0f;
+    if (item && n16 > 0) {
+        const uint16_t* wp = w + int64_t(c) * common + k0 + 8 * h;
+        const uint16_t* xp = x + k0 + 8 * h;
+        // NB steps of weights and x in flight (all 16 of a block for one or two
+        // rows), then their multiply-adds in order.  A block has at most 16
+        // steps; loads past its n16 repeat the last step (in bounds) and are
+        // not used.
+        constexpr int NB = R <= 2 ? 16 : 8;
+#pragma unroll
+        for (int i0 = 0; i0 < 16; i0 += NB) {
+            if (i0 >= n16) break;  // uniform over the kernel but for the last block
+            uint4 wq[NB], xq[R][NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int i = min(i0 + u, n16 - 1);
+                wq[u] = *reinterpret_cast<const uint4*>(wp + 16 * i);
+#pragma unroll
+                for (int r = 0; r < R; ++r) xq[r][u] = *reinterpret_cast<const uint4*>(xp + int64_t(r) * common + 16 * i);
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const bool on = i0 + u < n16;
+                float wf[8];
+                bf16x8_to_f32(wq[u], wf);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float xf[8];
+                    bf16x8_to_f32(xq[r][u], xf);
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        const float f = __builtin_fmaf(xf[l], wf[l], s[r][l]);
+                        s[r][l] = on ? f : s[r][l];
+                    }
+                }
+            }
+        }
+    }
+    // v = sum0 + sum1 (partner lane t ^ 1), the block's tree value
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float v[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const float o = __shfl_xor(s[r][l], 1);
+            v[l] = h == 0 ? s[r][l] + o : o + s[r][l];
+        }
+        float h2 = 0.0f;
+        if (item && h == 0 && rem8) {  // the trailing 8-element group, products rounded
+            const int k8 = k0 + 16 * n16;
+            float wf[8], xf[8];
+            bf16x8_to_f32(*reinterpret_cast<const uint4*>(w + int64_t(c) * common + k8), wf);
+            bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + int64_t(r) * common + k8), xf);
+            float pr[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) pr[l] = xf[l] * wf[l];
+            h2 = tree8(pr);
+        }
+        if (h == 0) {
+            s_h1[r][pair] = tree8(v);
+            s_h2[r][pair] = h2;
+        }
+    }
+    __syncthreads();
+    // one lane per column adds the blocks in order, then the bias, then rounds
+    if (t < cols_per_wg && col0 + t < cols) {
+        const int cc = col0 + t;
+        const float bv = bias ? bf16_to_f32(bias[cc]) : 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float acc = 0.0f;
+            for (int bb = 0; bb < nb; ++bb) {
+                const int kl = min(kBlockK, common - bb * kBlockK);
+                if (kl >= 16) acc += s_h1[r][t * nb + bb];
+                if (kl - 16 * (kl >> 4) >= 8) acc += s_h2[r][t * nb + bb];
+            }
+            float val = acc;
+            if (bias) val += bv;
+            out[int64_t(r) * cols + cc] = uint16_t(f32_to_bf16_ref(val));
+        }
+    }
+}
+
+// out = bf16(acc + bias) over the fp32 GEMM result [rows][cols]
+__global__ __launch_bounds__(256) void linear_epilogue_kernel(const float* __restrict__ acc,
+                                                              const uint16_t* __restrict__ bias,
+                                                              uint16_t* __restrict__ out, int64_t n, int cols) {
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+        float v = acc[i];
+        if (bias) v += bf16_to_f32(bias[i % cols]);
+        out[i] = uint16_t(f32_to_bf16_ref(v));
+    }
+}
+
+// one rocBLAS handle per device, created on first use
+std::mutex g_blas_mu;
+std::map<int, rocblas_handle> g_blas;
+
+int blas_handle(rocblas_handle* out) {
+    int dev = 0;
+    GENLLM_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_blas_mu);
+    auto it = g_blas.find(dev);
+    if (it == g_blas.end()) {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success)
+            return fail(GENLLM_ERR_HIP, "linear: rocblas_create_handle failed");
+        rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);  // deterministic sums
+        it = g_blas.emplace(dev, h).first;
+    }
+    *out = it->second;
+    return GENLLM_OK;
+}
+
+bool gemv_shape(int64_t rows, int64_t common) {
+    const int64_t nb = (common + kBlockK - 1) / kBlockK;
+    return rows >= 1 && rows <= kGemvRows && common % 8 == 0 && 2 * nb <= kGemvThreads;
+}
+
+}  // namespace
+
+size_t linear_workspace_bytes(int64_t rows, int64_t common, int64_t cols) {
+    if (rows <= 0 || common <= 0 || cols <= 0 || gemv_shape(rows, common)) return 0;
+    return size_t(rows) * size_t(cols) * sizeof(float);
+}
+
+int launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int64_t rows,
+                  int64_t common, int64_t cols, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!x || !w || !out) return fail(GENLLM_ERR_INVALID, "linear: null pointer");
+    if (rows < 0 || common <= 0 || cols < 0) return fail(GENLLM_ERR_INVALID, "linear: negative or zero size");
+    if (rows == 0 || cols == 0) return GENLLM_OK;
+    if (rows > INT32_MAX || common > INT32_MAX || cols > INT32_MAX)
+        return fail(GENLLM_ERR_INVALID, "linear: sizes must fit in 32 bits");
+    if (gemv_shape(rows, common)) {
+        const int nb = int((common + kBlockK - 1) / kBlockK);
+        const int cpw = kGemvThreads / (2 * nb);
+        const unsigned grid = unsigned((cols + cpw - 1) / cpw);
+        const int c = int(common), n = int(cols);
+        switch (rows) {
+            case 1: hipLaunchKernelGGL(linear_gemv_kernel<1>, dim3(grid), dim3(kGemvThreads), 0, stream, x, w, bias, out, c, n, nb, cpw); break;
+            case 2: hipLaunchKernelGGL(linear_gemv_kernel<2>, dim3(grid), dim3(kGemvThreads), 0, stream, x, w, bias, out, c, n, nb, cpw); break;
+            case 3: hipLaunchKernelGGL(linear_gemv_kernel<3>, dim3(grid), dim3(kGemvThreads), 0, stream, x, w, bias, out, c, n, nb, cpw); break;
+            default: hipLaunchKernelGGL(linear_gemv_kernel<4>, dim3(grid), dim3(kGemvThreads), 0, stream, x, w, bias, out, c, n, nb, cpw); break;
+        }
+        GENLLM_LAUNCH_CHECK("linear_gemv_kernel");
+        return GENLLM_OK;
+    }
+    const size_t need = linear_workspace_bytes(rows, common, cols);
+    if (!workspace || workspace_bytes < need)
+        return fail(GENLLM_ERR_INVALID, "linear: workspace too small (need " + std::to_string(need) + " bytes, have " +
+                                            std::to_string(workspace_bytes) + ")");
+    rocblas_handle hb = nullptr;
+    if (int rc = blas_handle(&hb)) return rc;
+    if (rocblas_set_stream(hb, stream) != rocblas_status_success)
+        return fail(GENLLM_ERR_HIP, "linear: rocblas_set_stream failed");
+    const float alpha = 1.0f, beta = 0.0f;
+    float* acc = static_cast<float*>(workspace);
+    // column-major view: acc^T [cols][rows] = (w as [common][cols])^T * (x as [common][rows])
+    const rocblas_status st = rocblas_gemm_ex(
+        hb, rocblas_operation_transpose, rocblas_operation_none, rocblas_int(cols), rocblas_int(rows),
+        rocblas_int(common), &alpha, w, rocblas_datatype_bf16_r, rocblas_int(common), x, rocblas_datatype_bf16_r,
+        rocblas_int(common), &beta, acc, rocblas_datatype_f32_r, rocblas_int(cols), acc, rocblas_datatype_f32_r,
+        rocblas_int(cols), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return fail(GENLLM_ERR_HIP, std::string("linear: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+    const int64_t n = rows * cols;
+    const unsigned grid = unsigned(std::min<int64_t>((n + 255) / 256, 4096));
+    hipLaunchKernelGGL(linear_epilogue_kernel, dim3(grid), dim3(256), 0, stream, acc, bias, out, n, int(cols));
+    GENLLM_LAUNCH_CHECK("linear_epilogue_kernel");
+    return GENLLM_OK;
+}
+
+}  // namespace genllm
+
+// ------------------------------------------------------------------- C ABI
+
+extern "C" size_t genllm_linear_workspace_bytes(int64_t rows, int64_t common, int64_t cols) {
+    return genllm::linear_workspace_bytes(rows, common, cols);
+}
+
+extern "C" int genllm_linear(const void* x, const void* w, const void* bias, void* out, int64_t rows, int64_t common,
+                             int64_t cols, void* workspace, size_t workspace_bytes, void* stream) {
+    return genllm::launch_linear(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                                 static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(out), rows, common, cols,
+                                 workspace, workspace_bytes, genllm::as_stream(stream));
+}

@@ -15,6 +15,7 @@ template <Device D> struct FlashAttentionImpl;
 template <Device D> struct RmsNormImpl;
 template <Device D> struct ApplyRopeImpl;
 template <Device D> struct RopeCacheImpl;
+template <Device D> struct LinearImpl;
 
 // src = {Q [1,Hq,S,D], K [1,Hkv,S,D], V [1,Hkv,S,D]}, op_params = {head_dim,
 // scale, causal, groups}; appends K/V to layer out->layer_id, then attends
@@ -45,6 +46,15 @@ template <> struct ApplyRopeImpl<Device::HIP> {
 // contains "_cos", else sin (rope.cpp:121-148).  Computed in double on the
 // host like the reference, then copied to out->data.
 template <> struct RopeCacheImpl<Device::HIP> {
+    static void execute(Tensor* out, int32_t dev_id);
+};
+
+// src = {x [1,M,common] bf16, w [cols,common] bf16, bias [cols] or null},
+// op_params[0] = transpose_w (must be 1, as the CPU op asserts), out
+// [1,M,cols] (linear.cpp:325-345, linear.cu:72-126).  Decode-sized M runs the
+// reference's summation order exactly; larger M a rocBLAS GEMM whose fp32
+// workspace this backend keeps per device.
+template <> struct LinearImpl<Device::HIP> {
     static void execute(Tensor* out, int32_t dev_id);
 };
 

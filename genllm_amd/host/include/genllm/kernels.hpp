@@ -33,6 +33,7 @@ void apply_rope(Tensor* out, int32_t dev_id = 0);
 void rope_cache(Tensor* out, int32_t dev_id = 0);
 void paged_attention(Tensor* out, int32_t dev_id = 0);  // append + attend over the paged cache
 void flash_attention(Tensor* out, int32_t dev_id = 0);  // attention over the node's own K/V
+void linear(Tensor* out, int32_t dev_id = 0);           // the Q/K/V projections feeding the attention
 
 // Executor::dispatch_kernel for these op types; false for any other op type.
 bool dispatch(Tensor* t, int32_t dev_id = 0);

@@ -7,8 +7,10 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <map>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "genllm/kernels.hpp"
@@ -126,6 +128,38 @@ void RopeCacheImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
         throw std::runtime_error("rope_cache: copy to the device failed");
 }
 
+// src/backend/cpu/linear.cpp:325-345 (batch 1, transpose_w), linear.cu:72-126
+void LinearImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
+    const Tensor* x = out->src[0];
+    const Tensor* w = out->src[1];
+    const Tensor* bias = out->src[2];
+    require_bf16(x, "linear");
+    require_bf16(w, "linear");
+    require_bf16(out, "linear");
+    if (int32_t(out->op_params[0]) != 1) throw std::runtime_error("linear: only transpose_w = 1 is supported");
+    if (x->dims[0] != 1) throw std::runtime_error("linear: batch must be 1");  // linear.cpp:332 asserts it
+    const int64_t rows = x->dims[1], common = x->dims[2], cols = w->dims[0];
+    const void* bp = bias && bias->data ? bias->data : nullptr;
+    if (bp) require_bf16(bias, "linear");
+    void* stream = device_stream(out, dev_id);
+    // fp32 workspace of the GEMM path, grown on demand; the old buffer is freed
+    // only after the stream has finished with it
+    static std::map<int32_t, std::pair<void*, size_t>> workspaces;
+    const size_t need = genllm_linear_workspace_bytes(rows, common, cols);
+    auto& ws = workspaces[dev_id];
+    if (need > ws.second) {
+        if (ws.first) {
+            if (hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess || hipFree(ws.first) != hipSuccess)
+                throw std::runtime_error("linear: releasing the old workspace failed");
+            ws = {nullptr, 0};
+        }
+        if (hipMalloc(&ws.first, need) != hipSuccess) throw std::runtime_error("linear: workspace allocation failed");
+        ws.second = need;
+    }
+    genllm_check(genllm_linear(x->data, w->data, bp, out->data, rows, common, cols, ws.first, ws.second, stream),
+                 "linear");
+}
+
 }  // namespace ops
 
 namespace kernel {
@@ -146,6 +180,9 @@ void paged_attention(Tensor* t, int32_t dev_id) {
 void flash_attention(Tensor* t, int32_t dev_id) {
     device::dispatchOp(t->device, [&]<Device D>() { ops::FlashAttentionImpl<D>::execute(t, dev_id); });
 }
+void linear(Tensor* t, int32_t dev_id) {
+    device::dispatchOp(t->device, [&]<Device D>() { ops::LinearImpl<D>::execute(t, dev_id); });
+}
 
 // src/core/executor.cpp:475-505
 bool dispatch(Tensor* t, int32_t dev_id) {
@@ -155,6 +192,7 @@ bool dispatch(Tensor* t, int32_t dev_id) {
         case OperationType::OP_TYPE_ROPE_CACHE: rope_cache(t, dev_id); return true;
         case OperationType::OP_TYPE_FLASH_ATTN: flash_attention(t, dev_id); return true;
         case OperationType::OP_TYPE_PAGED_ATTN: paged_attention(t, dev_id); return true;
+        case OperationType::OP_TYPE_LINEAR: linear(t, dev_id); return true;
         default: return false;
     }
 }

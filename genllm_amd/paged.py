@@ -294,6 +294,27 @@ def flash_attention(q, k, v, out, n_kv_groups: int, scale: float, causal: bool =
          float(scale), int(causal), _stream(stream))
 
 
+def linear_workspace_bytes(rows: int, common: int, cols: int) -> int:
+    return lib().genllm_linear_workspace_bytes(rows, common, cols)
+
+
+def linear(x, w, out, bias=None, workspace=None, stream=None):
+    """LinearImpl (linear.cpp:46-122, linear.cu:72-126) on contiguous bf16
+    tensors: x [rows, common], w [cols, common], bias [cols] or None,
+    out [rows, cols]; workspace: a device buffer of at least
+    linear_workspace_bytes(rows, common, cols) bytes when that is non-zero."""
+    rows, common = x.shape
+    cols = w.shape[0]
+    for t, shape in ((x, (rows, common)), (w, (cols, common)), (out, (rows, cols))):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise ValueError(f"linear: expected contiguous bf16 {shape}, got {tuple(t.shape)} {t.dtype}")
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (cols,)):
+        raise ValueError("linear: bias must be bf16 [cols]")
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    call("genllm_linear", _ptr(x), _ptr(w), _ptr(bias), _ptr(out), rows, common, cols, _ptr(workspace), ws_bytes,
+         _stream(stream))
+
+
 def fill_normal_bf16(t: torch.Tensor, seed: int, offset: int = 0, stream=None):
     call("genllm_fill_normal_bf16", _ptr(t), t.numel(), seed, offset, _stream(stream))
 

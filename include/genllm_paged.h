@@ -192,6 +192,22 @@ int genllm_flash_attention(const void *q, const void *k, const void *v, void *ou
                            int32_t n_q_heads, int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
                            int32_t n_kv_groups, float scale, int32_t causal, void *stream);
 
+/* ---------------------------------------------------------------- linear
+ * LinearImpl<D>::execute (src/backend/cpu/linear.cpp:46-122 and :325-345,
+ * src/backend/cuda/linear.cu:72-126), the Q/K/V projections in front of the
+ * attention op (Qwen3.cpp:130-134): out[r][c] = bf16(sum_k x[r][k] w[c][k] +
+ * bias[c]) with x [rows][common], w [cols][common] (the reference's
+ * transpose_w = 1 layout, one weight row per output), bias [cols] or NULL,
+ * out [rows][cols], all bf16 on the device; fp32 accumulation, the bias added
+ * in fp32, one rounding.  rows <= 4 with common % 8 == 0: the reference CPU
+ * summation order exactly (bit-identical results) and no workspace.  Other
+ * shapes: rocBLAS GEMM into an fp32 workspace of
+ * genllm_linear_workspace_bytes(rows, common, cols) bytes (0 when none is
+ * needed); GENLLM_ERR_INVALID if it is missing or smaller. */
+size_t genllm_linear_workspace_bytes(int64_t rows, int64_t common, int64_t cols);
+int genllm_linear(const void *x, const void *w, const void *bias, void *out, int64_t rows, int64_t common,
+                  int64_t cols, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ------------------------------------------------------------ utilities
  * No counterpart in the reference: synthetic seeded inputs for tests and the
  * benchmark (counter-based hash -> Box-Muller -> RNE bf16). */

@@ -87,6 +87,7 @@ def _declare(L):
         "or_paged_attend": (C.c_int, [_P, _i32, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, C.c_int]),
         "or_flash_attention": (None, [_P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, C.c_int]),
         "or_qk_norm_rope_append": (None, [_P, _i32, _P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _P, _f, _P, _P, _i64]),
+        "or_linear_bf16": (None, [_P, _P, _P, _i64, _i64, _i64, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -138,6 +139,21 @@ def apply_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, start_pos: int) 
     H, S, D = x.shape
     out = np.empty_like(x)
     lib().or_apply_rope(ptr(out), ptr(x), ptr(cos), ptr(sin), H, S, D, start_pos)
+    return out
+
+
+def linear(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """x [rows][common], w [cols][common], bias [cols] (bf16 bits) -> out [rows][cols]."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    rows, common = x.shape
+    cols = w.shape[0]
+    assert w.shape[1] == common
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.uint16)
+        assert bias.shape == (cols,)
+    out = np.empty((rows, cols), dtype=np.uint16)
+    lib().or_linear_bf16(ptr(out), ptr(x), ptr(w), rows, common, cols, ptr(bias))
     return out
 
 

@@ -128,6 +128,12 @@ void or_qk_norm_rope_append(or_manager *m, int32_t layer, const uint16_t *q_tok,
                             const float *gamma_k, float eps, const float *cos_tab, const float *sin_tab,
                             int64_t start_pos);
 
+/* ---- linear<bfloat16_t>: src/backend/cpu/linear.cpp:46-122 (LinearImpl<CPU>, :325-345) ----
+ * x [rows][common], w [cols][common] (transpose_w = 1), bias [cols] or NULL,
+ * out [rows][cols]; the reference's fp32 summation order, one rounding. */
+void or_linear_bf16(uint16_t *out, const uint16_t *x, const uint16_t *w, int64_t rows, int64_t common, int64_t cols,
+                    const uint16_t *bias);
+
 #ifdef __cplusplus
 }
 #endif

@@ -371,6 +371,49 @@ bool test_rms_norm_rope_nodes() {
     return true;
 }
 
+// ------------------------------------------------------------------- Linear
+// LINEAR node (linear.cpp:325-345): decode-sized M bit-exact against the
+// oracle's restatement of the reference's summation order; a prefill-sized M
+// through the GEMM path within one bf16 rounding of it.
+bool run_linear(int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_t seed, bool exact) {
+    MemoryManager mm;
+    DevBuf x(size_t(M * common * 2)), w(size_t(cols * common * 2)), b(size_t(cols * 2)), o(size_t(M * cols * 2));
+    auto hx = fill_normal(x, seed), hw = fill_normal(w, seed + 1), hb = fill_normal(b, seed + 2);
+    Tensor X = make_tensor(x.p, {1, M, common, 0}), W = make_tensor(w.p, {cols, common, 0, 0}),
+           Bv = make_tensor(b.p, {cols, 0, 0, 0});
+    Tensor out = make_tensor(o.p, {1, M, cols, 0});
+    out.op_type = OperationType::OP_TYPE_LINEAR;
+    out.src = {&X, &W, with_bias ? &Bv : nullptr, nullptr, nullptr, nullptr};
+    out.op_params = {1.0f, 0, 0, 0};  // transpose_w
+    ASSERT(kernel::dispatch(&out, 0), "executor dispatches LINEAR");
+    std::vector<uint16_t> want(size_t(M * cols));
+    or_linear_bf16(want.data(), hx.data(), hw.data(), M, common, cols, with_bias ? hb.data() : nullptr);
+    const auto got = to_host<uint16_t>(o.p, want.size());
+    if (exact) {
+        ASSERT(got == want, "linear bit-exact against the oracle");
+    } else {
+        // both sides are one bf16 rounding of an fp32 sum: |got - want| <= one
+        // bf16 ulp of the larger plus twice the fp32 accumulation bound
+        // common * 2^-24 * sum_k |x_k w_k|
+        size_t far = 0;
+        for (int64_t r = 0; r < M; ++r)
+            for (int64_t c = 0; c < cols; ++c) {
+                double mag = with_bias ? std::abs(double(or_bf16_to_f32(hb[c]))) : 0.0;
+                for (int64_t k = 0; k < common; ++k)
+                    mag += std::abs(double(or_bf16_to_f32(hx[r * common + k])) * or_bf16_to_f32(hw[c * common + k]));
+                const double a = or_bf16_to_f32(got[r * cols + c]), b = or_bf16_to_f32(want[r * cols + c]);
+                const double big = std::max(std::abs(a), std::abs(b));
+                const double ulp = std::ldexp(1.0, std::ilogb(std::max(big, 1e-38)) - 7);
+                if (std::abs(a - b) > ulp + 2.0 * double(common) * std::ldexp(1.0, -24) * mag) ++far;
+            }
+        ASSERT(far == 0, "linear GEMM within one bf16 rounding + fp32 accumulation error of the oracle");
+    }
+    return true;
+}
+
+bool test_linear_decode() { return run_linear(1, 2560, 1024, false, 31, true) && run_linear(3, 1024, 300, true, 32, true); }
+bool test_linear_prefill() { return run_linear(64, 1024, 512, true, 33, false); }
+
 }  // namespace
 
 int main() {
@@ -394,5 +437,7 @@ int main() {
         {"flash attention full", test_flash_attention_full},
         {"flash attention one token", test_flash_attention_one_token},
         {"rms_norm / rope_cache / apply_rope nodes", test_rms_norm_rope_nodes},
+        {"linear node, decode rows (bit-exact)", test_linear_decode},
+        {"linear node, prefill rows (GEMM)", test_linear_prefill},
     });
 }

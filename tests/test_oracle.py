@@ -432,3 +432,76 @@ def test_qk_norm_rope_append_composition(orc):
         g = 5 + t
         assert np.array_equal(kp[k_ids[g // 16], g % 16], k_rope[:, t])
         assert np.array_equal(vp[v_ids[g // 16], g % 16], v[t])
+
+
+# ---------------------------------------------------------------- linear
+def _linear_ref_int(x, w, bias):
+    """Exact integer dot products (inputs are small integers, exact in bf16
+    and fp32; every partial sum stays below 2^24, so any fp32 summation order
+    gives this value), rounded by the independent nearest-bf16 definition."""
+    acc = x.astype(np.int64) @ w.astype(np.int64).T
+    if bias is not None:
+        acc = acc + bias.astype(np.int64)[None, :]
+    u = acc.astype(np.float32).view(np.uint32)
+    out = nearest_bf16_bruteforce(u.ravel()).reshape(acc.shape)
+    return np.where(acc == 0, np.uint16(0), out)
+
+
+@pytest.mark.parametrize("common", [5, 8, 13, 16, 24, 40, 256, 264, 272, 300, 520, 2560])
+def test_linear_integer_closed_form(orc, common):
+    # every path of linear.cpp:66-114: 16-element steps, the trailing 8-group,
+    # the scalar tail, several K-blocks, the bias
+    rng = np.random.default_rng(common)
+    rows, cols = 3, 37
+    x = rng.integers(-4, 5, size=(rows, common))
+    w = rng.integers(-4, 5, size=(cols, common))
+    bias = rng.integers(-50, 51, size=cols)
+    to_bits = lambda a: synth.f32_to_bf16_bits(a.astype(np.float32))
+    got = orc.linear(to_bits(x), to_bits(w), to_bits(bias))
+    assert np.array_equal(got, _linear_ref_int(x, w, bias))
+    got_nb = orc.linear(to_bits(x), to_bits(w))
+    assert np.array_equal(got_nb, _linear_ref_int(x, w, None))
+
+
+def test_linear_block_and_tree_order(orc):
+    # Order pins derived by hand from linear.cpp:66-114.  Block 0 holds
+    # x*w = 2^24 at k=0 (sum0 lane 0) and 1 at k=8 and k=24 (sum1 lane 0, steps 0
+    # and 1); block 1 holds -2^24 at k=256.  The reference forms sum1 lane 0 =
+    # 1 + 1 = 2 first, v0 = 2^24 + 2 (exact), block 0 adds 16777218, block 1
+    # brings it back to 2.  A flat left-to-right sum would give
+    # ((2^24 + 1) + 1) - 2^24 = 0 in fp32.
+    common = 512
+    x = np.zeros((1, common), dtype=np.float32)
+    w = np.zeros((1, common), dtype=np.float32)
+    x[0, 0], w[0, 0] = 4096.0, 4096.0
+    x[0, 8], w[0, 8] = 1.0, 1.0
+    x[0, 24], w[0, 24] = 1.0, 1.0
+    x[0, 256], w[0, 256] = 4096.0, -4096.0
+    to_bits = lambda a: synth.f32_to_bf16_bits(a)
+    assert f32(orc.linear(to_bits(x), to_bits(w)))[0, 0] == 2.0
+    # the same 1s in lanes that meet the big value before each other (k=1 is
+    # sum0 lane 1; t1 = v1 + v5 = 1, then (t0 + t1) = 2^24 + 1 -> 2^24): 0
+    x2, w2 = x.copy(), w.copy()
+    x2[0, 8] = w2[0, 8] = 0.0
+    x2[0, 1], w2[0, 1] = 1.0, 1.0
+    x2[0, 24] = w2[0, 24] = 0.0
+    assert f32(orc.linear(to_bits(x2), to_bits(w2)))[0, 0] == 0.0
+    # a small value in block 1 (after the big one is already in the running
+    # sum): block 1 = -2^24 + 1 = -16777215 exactly, total 1
+    x3, w3 = x2.copy(), w2.copy()
+    x3[0, 1] = w3[0, 1] = 0.0
+    x3[0, 257], w3[0, 257] = 1.0, 1.0
+    assert f32(orc.linear(to_bits(x3), to_bits(w3)))[0, 0] == 1.0
+
+
+def test_linear_fp64_bound(orc):
+    rng = np.random.default_rng(5)
+    rows, common, cols = 2, 2560, 64
+    x = synth.f32_to_bf16_bits(rng.standard_normal((rows, common)).astype(np.float32))
+    w = synth.f32_to_bf16_bits((rng.standard_normal((cols, common)) * 0.05).astype(np.float32))
+    got = f32(orc.linear(x, w)).astype(np.float64)
+    xf, wf = f32(x).astype(np.float64), f32(w).astype(np.float64)
+    exact = xf @ wf.T
+    mag = np.abs(xf) @ np.abs(wf).T
+    # one bf16 rounding plus fp32 accumulation error (well under common * 2^-24 * mag)
+    assert np.all(np.abs(got - exact) <= bf16_ulp(exact) / 2 + common * 2.0 ** -24 * mag)
