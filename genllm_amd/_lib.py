@@ -84,9 +84,9 @@ SIGNATURES = {
     "genllm_kv_block_free": (_int, [_P, _i32, _i32, _i32]),
     "genllm_paged_attention": (_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, _i32, _P]),
     "genllm_qk_norm_rope_append": (_int, [_P, _i32, _i32, _P, _i64, _i64, _P, _i64, _i64, _P, _P, _i64, _i64,
-                                          _i32, _P, _P, _i64, _i64, _f, _P, _P, _i64, _P]),
+                                          _i32, _P, _P, _i64, _i64, _f, _P, _P, _i32, _i64, _P]),
     "genllm_rms_norm": (_int, [_P, _P, _P, _i64, _i32, _f, _P]),
-    "genllm_apply_rope": (_int, [_P, _P, _P, _P, _i32, _i32, _i32, _i64, _P]),
+    "genllm_apply_rope": (_int, [_P, _P, _P, _P, _i32, _i32, _i32, _i32, _i64, _P]),
     "genllm_rope_cache": (_int, [_P, _f, _i32, _i32, _i32]),
     "genllm_kv_scatter": (_int, [_P, _i64, _i64, _P, _i64, _i64, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _P]),
     "genllm_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),

@@ -35,8 +35,9 @@ struct AppendParams {
     float eps = 0.0f;
     const float* cos_tab = nullptr;
     const float* sin_tab = nullptr;
-    int64_t rope_stride = 0;  // elements per table row
+    int64_t rope_stride = 0;  // elements per table row (= the rotated dims)
     int64_t rope_pos0 = 0;
+    int32_t rope_dim = 0;     // leading dims rotated (pairs i, i + rope_dim/2); the rest pass through
     int32_t S = 0, Hkv = 0, Hq = 0;
     int32_t pos0 = 0;         // cache position of token 0
     int32_t nq_tasks = 0, nkv_tasks = 0;
@@ -98,6 +99,6 @@ int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream);
 int launch_rms_norm(uint16_t* out, const uint16_t* x, const float* w, int64_t rows, int hidden, float eps,
                     hipStream_t stream);
 int launch_apply_rope(uint16_t* out, const uint16_t* x, const float* cos_tab, const float* sin_tab, int n_heads,
-                      int seq_len, int head_dim, int64_t start_pos, hipStream_t stream);
+                      int seq_len, int head_dim, int rope_dim, int64_t start_pos, hipStream_t stream);
 
 }  // namespace genllm

@@ -18,7 +18,10 @@
 // 8-lane shuffles reproduce the reference's combine order
 //   T[k] = (A[k]+A[8+k]) + (A[16+k]+A[24+k]),  ss = ((T0+T4)+(T1+T5)) + ((T2+T6)+(T3+T7))
 // bit for bit.  The NeoX pair (i, i+D/2) is (t, t+D/64) in the same lane, so
-// RoPE needs no exchange.  Rounding follows the reference: truncation to bf16
+// RoPE needs no exchange; a partial rotation over the first rope_dim dims
+// (Qwen3.5: 64 of 256, Qwen35.hpp:14-16) pairs (i, i+rope_dim/2) = (t,
+// t+rope_dim/64) with table rows of rope_dim floats and leaves the other dims
+// as normed.  Rounding follows the reference: truncation to bf16
 // after the norm, then RNE (subnormal flush) after RoPE, with the rotation
 // contracted as GCC contracts the CPU op: fma(x0,c,-(x1*s)), fma(x0,s,x1*c).
 //
@@ -40,10 +43,14 @@ namespace {
 
 constexpr int TPW = 4;  // tasks per wave
 
-template <int D>
+// TR = rope_dim / 64: chunk t < TR of a lane rotates with chunk t + TR (the
+// pair (i, i + rope_dim/2)); chunks from 2 TR on pass through.  TR = D/64 is
+// the reference's full rotation.
+template <int D, int TR>
 struct Append {
     static constexpr int R = D / 32;  // 8-byte chunks per q/k row and lane
     static constexpr int U = D / 64;  // 16-byte chunks per v row and lane
+    static_assert(TR >= 1 && 2 * TR <= R, "rotated chunks");
 
     // Block id of local page lp (K: which = 0, V: 1): opened by this call ->
     // from the launch arguments, else from the device table.  -1 when the id
@@ -70,7 +77,7 @@ struct Append {
     // RMSNorm (optional, gamma chunks gw) + RoPE (optional, table chunks c4/s4
     // of the row's position) of one row, in place.
     __device__ __forceinline__ static void norm_rope(uint2 (&x)[R], bool norm, const float4 (&gw)[R], float eps, bool rope,
-                                     const float4 (&c4)[R / 2], const float4 (&s4)[R / 2]) {
+                                     const float4 (&c4)[TR], const float4 (&s4)[TR]) {
         float v[R][4];
 #pragma unroll
         for (int t = 0; t < R; ++t) {
@@ -109,23 +116,22 @@ struct Append {
             }
         }
         uint32_t o[R][4];
+#pragma unroll
+        for (int t = 0; t < R; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[t][q] = __float_as_uint(v[t][q]) >> 16;  // unrotated: exact
         if (rope) {
 #pragma unroll
-            for (int t = 0; t < R / 2; ++t) {
+            for (int t = 0; t < TR; ++t) {
                 const float c[4] = {c4[t].x, c4[t].y, c4[t].z, c4[t].w};
                 const float s[4] = {s4[t].x, s4[t].y, s4[t].z, s4[t].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const float x0 = v[t][q], x1 = v[t + R / 2][q];
+                    const float x0 = v[t][q], x1 = v[t + TR][q];
                     o[t][q] = f32_to_bf16_ref(__builtin_fmaf(x0, c[q], -(x1 * s[q])));
-                    o[t + R / 2][q] = f32_to_bf16_ref(__builtin_fmaf(x0, s[q], x1 * c[q]));
+                    o[t + TR][q] = f32_to_bf16_ref(__builtin_fmaf(x0, s[q], x1 * c[q]));
                 }
             }
-        } else {
-#pragma unroll
-            for (int t = 0; t < R; ++t)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) o[t][q] = __float_as_uint(v[t][q]) >> 16;
         }
 #pragma unroll
         for (int t = 0; t < R; ++t) {
@@ -164,7 +170,7 @@ struct Append {
             // Every load of the wave is issued before any arithmetic: the rows,
             // gamma (once) and the RoPE table chunks of each row's position.
             uint2 x[TPW][R];
-            float4 c4[TPW][R / 2], s4[TPW][R / 2];
+            float4 c4[TPW][TR], s4[TPW][TR];
             int tok[TPW], h[TPW];
             bool ok[TPW];
             const bool rope = p.cos_tab != nullptr;
@@ -186,7 +192,7 @@ struct Append {
                     const bool live = t0 + u < n_kind;
                     const int64_t row = (p.rope_pos0 + (live ? tok[u] : 0)) * p.rope_stride + 4 * j;
 #pragma unroll
-                    for (int c = 0; c < R / 2; ++c) {
+                    for (int c = 0; c < TR; ++c) {
                         c4[u][c] = *reinterpret_cast<const float4*>(p.cos_tab + row + 32 * c);
                         s4[u][c] = *reinterpret_cast<const float4*>(p.sin_tab + row + 32 * c);
                     }
@@ -235,9 +241,9 @@ struct Append {
     }
 };
 
-template <int D>
+template <int D, int TR>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
-    Append<D>::run(p);
+    Append<D, TR>::run(p);
 }
 
 }  // namespace
@@ -250,11 +256,20 @@ int launch_kv_append(const AppendParams& p, int head_dim, hipStream_t stream) {
         if (p.upd.count == 0) return GENLLM_OK;
         blocks = 1;  // table update only
     }
-    switch (head_dim) {
-        case 64: hipLaunchKernelGGL(kv_append_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, stream, p); break;
-        case 128: hipLaunchKernelGGL(kv_append_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, stream, p); break;
-        case 256: hipLaunchKernelGGL(kv_append_kernel<256>, dim3(unsigned(blocks)), dim3(256), 0, stream, p); break;
-        default: return fail(GENLLM_ERR_UNSUPPORTED, "kv append: head_dim must be 64, 128 or 256");
+    // rope_dim: the rotated dims (head_dim for the reference's full rotation;
+    // without tables it does not matter)
+    const int rd = p.cos_tab ? (p.rope_dim ? p.rope_dim : head_dim) : head_dim;
+    const dim3 g{unsigned(blocks)}, b{256u};
+    switch (head_dim * 1000 + rd) {
+        case 64 * 1000 + 64: hipLaunchKernelGGL((kv_append_kernel<64, 1>), g, b, 0, stream, p); break;
+        case 128 * 1000 + 64: hipLaunchKernelGGL((kv_append_kernel<128, 1>), g, b, 0, stream, p); break;
+        case 128 * 1000 + 128: hipLaunchKernelGGL((kv_append_kernel<128, 2>), g, b, 0, stream, p); break;
+        case 256 * 1000 + 64: hipLaunchKernelGGL((kv_append_kernel<256, 1>), g, b, 0, stream, p); break;
+        case 256 * 1000 + 128: hipLaunchKernelGGL((kv_append_kernel<256, 2>), g, b, 0, stream, p); break;
+        case 256 * 1000 + 256: hipLaunchKernelGGL((kv_append_kernel<256, 4>), g, b, 0, stream, p); break;
+        default:
+            return fail(GENLLM_ERR_UNSUPPORTED,
+                        "kv append: head_dim must be 64, 128 or 256 and rope_dim a multiple of 64 up to it");
     }
     GENLLM_LAUNCH_CHECK("kv_append_kernel");
     return GENLLM_OK;

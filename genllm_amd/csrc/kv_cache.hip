@@ -542,8 +542,8 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
                                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                                           int32_t n_q_heads, const float* gamma_q, void* q_out,
                                           int64_t qo_tok_stride, int64_t qo_head_stride, float eps,
-                                          const float* cos_tab, const float* sin_tab, int64_t rope_pos0,
-                                          void* stream) {
+                                          const float* cos_tab, const float* sin_tab, int32_t rope_dim,
+                                          int64_t rope_pos0, void* stream) {
     if (!kv) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: null kv");
     LayerState* s = active_layer(kv, layer);
     if (!s) return GENLLM_OK;
@@ -555,6 +555,8 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     if (!k || !v) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: null k/v");
     if ((cos_tab == nullptr) != (sin_tab == nullptr))
         return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: cos and sin tables go together");
+    if (cos_tab && (rope_dim <= 0 || rope_dim > D || rope_dim % 64))
+        return fail(GENLLM_ERR_UNSUPPORTED, "qk_norm_rope_append: rope_dim must be a multiple of 64, at most head_dim");
     if (q && (!q_out || n_q_heads <= 0)) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: q needs q_out");
     if (!aligned(k, 8) || !aligned(v, 16) || (k_tok_stride % 4) || (k_head_stride % 4) || (v_tok_stride % 8) ||
         (v_head_stride % 8) || (q && (!aligned(q, 8) || !aligned(q_out, 8) || (q_tok_stride % 4) ||
@@ -583,7 +585,8 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     ap.eps = eps;
     ap.cos_tab = cos_tab;
     ap.sin_tab = sin_tab;
-    ap.rope_stride = D;
+    ap.rope_stride = cos_tab ? rope_dim : D;
+    ap.rope_dim = cos_tab ? rope_dim : D;
     ap.rope_pos0 = rope_pos0;
     ap.S = seq_len;
     ap.Hkv = s->n_kv_heads;
@@ -609,12 +612,13 @@ extern "C" int genllm_rms_norm(void* out, const void* x, const float* w, int64_t
 }
 
 extern "C" int genllm_apply_rope(void* out, const void* x, const float* cos_tab, const float* sin_tab,
-                                 int32_t n_heads, int32_t seq_len, int32_t head_dim, int64_t start_pos,
-                                 void* stream) {
-    if (!out || !x || !cos_tab || !sin_tab || head_dim <= 0 || head_dim % 2 || start_pos < 0)
+                                 int32_t n_heads, int32_t seq_len, int32_t head_dim, int32_t rope_dim,
+                                 int64_t start_pos, void* stream) {
+    if (!out || !x || !cos_tab || !sin_tab || head_dim <= 0 || head_dim % 2 || start_pos < 0 || rope_dim <= 0 ||
+        rope_dim % 2 || rope_dim > head_dim)
         return fail(GENLLM_ERR_INVALID, "apply_rope: bad arguments");
     return launch_apply_rope(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(x), cos_tab, sin_tab,
-                             n_heads, seq_len, head_dim, start_pos, as_stream(stream));
+                             n_heads, seq_len, head_dim, rope_dim, start_pos, as_stream(stream));
 }
 
 extern "C" int genllm_rope_cache(float* dst, float theta, int32_t head_dim, int32_t max_seq, int32_t is_cos) {

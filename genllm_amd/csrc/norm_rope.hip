@@ -58,20 +58,32 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t* out, const uint
     }
 }
 
+// One thread per slot i < head_dim/2 of a row.  Slots below rope_dim/2 rotate
+// the pair (i, i + rope_dim/2) with table entry [pos][i] (rows of rope_dim
+// floats); slot i >= rope_dim/2 copies the two elements rope_dim + 2(i -
+// rope_dim/2) + {0, 1} unchanged.  rope_dim == head_dim is the reference op.
 __global__ __launch_bounds__(256) void apply_rope_kernel(uint16_t* out, const uint16_t* x, const float* cos_tab,
                                                          const float* sin_tab, int64_t rows, int seq_len,
-                                                         int head_dim, int64_t start_pos) {
-    const int half = head_dim / 2;
+                                                         int head_dim, int rope_dim, int64_t start_pos) {
+    const int half = head_dim / 2, rhalf = rope_dim / 2;
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= rows * half) return;
     const int64_t row = idx / half;
     const int i = int(idx - row * half);
+    const uint16_t* xr = x + row * head_dim;
+    uint16_t* orow = out + row * head_dim;
+    if (i >= rhalf) {
+        const int e = rope_dim + 2 * (i - rhalf);
+        orow[e] = xr[e];
+        orow[e + 1] = xr[e + 1];
+        return;
+    }
     const int64_t pos = start_pos + row % seq_len;
-    const float c = cos_tab[pos * head_dim + i], s = sin_tab[pos * head_dim + i];
-    const float x0 = bf16_to_f32(x[row * head_dim + i]);
-    const float x1 = bf16_to_f32(x[row * head_dim + i + half]);
-    out[row * head_dim + i] = uint16_t(f32_to_bf16_ref(__builtin_fmaf(x0, c, -(x1 * s))));
-    out[row * head_dim + i + half] = uint16_t(f32_to_bf16_ref(__builtin_fmaf(x0, s, x1 * c)));
+    const float c = cos_tab[pos * rope_dim + i], s = sin_tab[pos * rope_dim + i];
+    const float x0 = bf16_to_f32(xr[i]);
+    const float x1 = bf16_to_f32(xr[i + rhalf]);
+    orow[i] = uint16_t(f32_to_bf16_ref(__builtin_fmaf(x0, c, -(x1 * s))));
+    orow[i + rhalf] = uint16_t(f32_to_bf16_ref(__builtin_fmaf(x0, s, x1 * c)));
 }
 
 int launch_rms_norm(uint16_t* out, const uint16_t* x, const float* w, int64_t rows, int hidden, float eps,
@@ -84,13 +96,13 @@ int launch_rms_norm(uint16_t* out, const uint16_t* x, const float* w, int64_t ro
 }
 
 int launch_apply_rope(uint16_t* out, const uint16_t* x, const float* cos_tab, const float* sin_tab, int n_heads,
-                      int seq_len, int head_dim, int64_t start_pos, hipStream_t stream) {
+                      int seq_len, int head_dim, int rope_dim, int64_t start_pos, hipStream_t stream) {
     const int64_t rows = int64_t(n_heads) * seq_len;
     const int64_t n = rows * (head_dim / 2);
     if (n <= 0) return GENLLM_OK;
     const int64_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(apply_rope_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream, out, x, cos_tab, sin_tab,
-                       rows, seq_len, head_dim, start_pos);
+                       rows, seq_len, head_dim, rope_dim, start_pos);
     GENLLM_LAUNCH_CHECK("apply_rope_kernel");
     return GENLLM_OK;
 }

@@ -105,12 +105,16 @@ void ApplyRopeImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     require_bf16(x, "apply_rope");
     require_bf16(out, "apply_rope");
     const int64_t head_dim = int64_t(out->op_params[0]);
+    // op_params[1] = rope_dim, the width of the tables (op_factory.hpp:504-529);
+    // the reference op reads it but indexes with head_dim, so only
+    // rope_dim == head_dim matches it -- a smaller one rotates the leading dims
+    const int64_t rope_dim = out->op_params[1] > 0 ? int64_t(out->op_params[1]) : head_dim;
     const int64_t start_pos = int64_t(out->op_params[2]);
     const int64_t B = x->dims[0], n_heads = x->dims[1], seq_len = x->dims[2];
     if (B != 1) throw std::runtime_error("apply_rope: batch must be 1");  // rope.cpp:89 asserts it
     genllm_check(genllm_apply_rope(out->data, x->data, static_cast<const float*>(cos->data),
                                    static_cast<const float*>(sin->data), int32_t(n_heads), int32_t(seq_len),
-                                   int32_t(head_dim), start_pos, device_stream(out, dev_id)),
+                                   int32_t(head_dim), int32_t(rope_dim), start_pos, device_stream(out, dev_id)),
                  "apply_rope");
 }
 

@@ -214,14 +214,17 @@ def paged_attention(mgr: PagedAttentionManager, layer: int, q, k, v, out, n_kv_g
 def qk_norm_rope_append(mgr: PagedAttentionManager, layer: int, k, v, gamma_k, eps: float, cos, sin,
                         rope_pos0: int, q=None, gamma_q=None, q_out=None, stream=None):
     """Fused per-head RMSNorm -> RoPE -> page scatter.  k, v: token-major
-    [S][Hkv][D]; q (optional) token-major [S][Hq][D]; q_out head-major [Hq][S][D]."""
+    [S][Hkv][D]; q (optional) token-major [S][Hq][D]; q_out head-major [Hq][S][D].
+    cos/sin [max_seq][rope_dim]: the first rope_dim dims rotate (all of them
+    when rope_dim == D)."""
     S, Hkv, D = k.shape
+    rope_dim = cos.shape[-1] if cos is not None else D
     Hq = q.shape[1] if q is not None else 0
     qs = (q.stride(0), q.stride(1)) if q is not None else (0, 0)
     qos = (q_out.stride(1), q_out.stride(0)) if q_out is not None else (0, 0)
     call("genllm_qk_norm_rope_append", mgr.handle, layer, S, _ptr(k), k.stride(0), k.stride(1), _ptr(v),
          v.stride(0), v.stride(1), _ptr(gamma_k), _ptr(q), qs[0], qs[1], Hq, _ptr(gamma_q), _ptr(q_out), qos[0],
-         qos[1], float(eps), _ptr(cos), _ptr(sin), int(rope_pos0), _stream(stream))
+         qos[1], float(eps), _ptr(cos), _ptr(sin), int(rope_dim), int(rope_pos0), _stream(stream))
 
 
 # ------------------------------------------------------- stateless kernels
@@ -231,9 +234,11 @@ def rms_norm(out, x, w, eps: float, stream=None):
 
 
 def apply_rope(out, x, cos, sin, start_pos: int, stream=None):
-    """x head-major [H][S][D]."""
+    """x head-major [H][S][D]; cos/sin [max_seq][rope_dim] (rope_dim <= D
+    leading dims rotate)."""
     H, S, D = x.shape
-    call("genllm_apply_rope", _ptr(out), _ptr(x), _ptr(cos), _ptr(sin), H, S, D, int(start_pos), _stream(stream))
+    call("genllm_apply_rope", _ptr(out), _ptr(x), _ptr(cos), _ptr(sin), H, S, D, int(cos.shape[-1]),
+         int(start_pos), _stream(stream))
 
 
 def rope_cache(theta: float, head_dim: int, max_seq: int):

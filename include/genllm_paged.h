@@ -124,15 +124,21 @@ int genllm_paged_attention(genllm_kv *kv, int32_t layer, const void *q, const vo
  * k, v: token-major [seq_len][n_kv_heads][head_dim] (pre-permute), strides in
  * elements.  q (optional, NULL to skip) has its own strides and is written,
  * normed and rotated, to q_out.  gamma_k/gamma_q may be NULL (no norm);
- * cos_tab/sin_tab may be NULL (no RoPE); tables are [max_seq][head_dim] fp32
- * as RopeCacheImpl builds them. */
+ * cos_tab/sin_tab may be NULL (no RoPE); tables are [max_seq][rope_dim] fp32
+ * as RopeCacheImpl builds them for rope_dim (the op's op_params[1],
+ * op_factory.hpp:504-529): the first rope_dim dims rotate in pairs
+ * (i, i + rope_dim/2), the others pass through.  rope_dim = head_dim is the
+ * Qwen3 layer; Qwen3.5 rotates 64 of 256 (Qwen35.hpp:14-16).  rope_dim must
+ * be a multiple of 64.  (The reference's ApplyRopeImpl ignores op_params[1]
+ * and indexes the table with stride head_dim, rope.cpp:80-101, so its
+ * partial form reads outside the table; that is not reproduced.) */
 int genllm_qk_norm_rope_append(genllm_kv *kv, int32_t layer, int32_t seq_len,
                                const void *k, int64_t k_tok_stride, int64_t k_head_stride,
                                const void *v, int64_t v_tok_stride, int64_t v_head_stride,
                                const float *gamma_k, const void *q, int64_t q_tok_stride, int64_t q_head_stride,
                                int32_t n_q_heads, const float *gamma_q, void *q_out, int64_t qo_tok_stride,
                                int64_t qo_head_stride, float eps, const float *cos_tab, const float *sin_tab,
-                               int64_t rope_pos0, void *stream);
+                               int32_t rope_dim, int64_t rope_pos0, void *stream);
 
 /* --------------------------------------------------- stateless kernels */
 
@@ -142,9 +148,11 @@ int genllm_qk_norm_rope_append(genllm_kv *kv, int32_t layer, int32_t seq_len,
 int genllm_rms_norm(void *out, const void *x, const float *w, int64_t rows, int32_t hidden, float eps,
                     void *stream);
 /* ApplyRopeImpl<D>::execute (rope.cpp:76-119): head-major [n_heads][seq_len][head_dim]
- * bf16, positions start_pos + s. */
+ * bf16, positions start_pos + s, op_params = {head_dim, rope_dim, start_pos}.
+ * Tables [max_seq][rope_dim]; the first rope_dim dims rotate, the others are
+ * copied (rope_dim = head_dim: the reference op; rope_dim even, <= head_dim). */
 int genllm_apply_rope(void *out, const void *x, const float *cos_tab, const float *sin_tab, int32_t n_heads,
-                      int32_t seq_len, int32_t head_dim, int64_t start_pos, void *stream);
+                      int32_t seq_len, int32_t head_dim, int32_t rope_dim, int64_t start_pos, void *stream);
 /* RopeCacheImpl<CPU>::execute (rope.cpp:121-148) into host memory, in double
  * precision like the reference; the caller copies it to the device once. */
 int genllm_rope_cache(float *host_dst, float theta, int32_t head_dim, int32_t max_seq, int32_t is_cos);

@@ -86,7 +86,9 @@ def _declare(L):
         "or_paged_attention": (C.c_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, C.c_int]),
         "or_paged_attend": (C.c_int, [_P, _i32, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, C.c_int]),
         "or_flash_attention": (None, [_P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, C.c_int]),
-        "or_qk_norm_rope_append": (None, [_P, _i32, _P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _P, _f, _P, _P, _i64]),
+        "or_qk_norm_rope_append": (None, [_P, _i32, _P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _P, _f, _P, _P, _i32,
+                                          _i64]),
+        "or_apply_rope_partial": (None, [_P, _P, _P, _P, _i64, _i64, _i64, _i64, _i64]),
         "or_linear_bf16": (None, [_P, _P, _P, _i64, _i64, _i64, _P]),
     }
     for name, (res, args) in sig.items():
@@ -154,6 +156,15 @@ def linear(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None) -> np.n
         assert bias.shape == (cols,)
     out = np.empty((rows, cols), dtype=np.uint16)
     lib().or_linear_bf16(ptr(out), ptr(x), ptr(w), rows, common, cols, ptr(bias))
+    return out
+
+
+def apply_rope_partial(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, start_pos: int) -> np.ndarray:
+    """x head-major [H][S][D] bf16 bits; tables [max_seq][rope_dim]."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    H, S, D = x.shape
+    out = np.empty_like(x)
+    lib().or_apply_rope_partial(ptr(out), ptr(x), ptr(cos), ptr(sin), H, S, D, cos.shape[1], start_pos)
     return out
 
 
@@ -311,6 +322,8 @@ class Manager:
             q_out = np.empty((Hq, S, D), dtype=np.uint16)
             gamma_q = np.ascontiguousarray(gamma_q, dtype=np.float32)
         gamma_k = np.ascontiguousarray(gamma_k, dtype=np.float32)
+        rope_dim = cos.shape[1] if cos is not None else D
         lib().or_qk_norm_rope_append(self._h, layer, ptr(q_tok), Hq, ptr(gamma_q), ptr(q_out), ptr(k_tok),
-                                     ptr(v_tok), Hkv, S, D, ptr(gamma_k), eps, ptr(cos), ptr(sin), start_pos)
+                                     ptr(v_tok), Hkv, S, D, ptr(gamma_k), eps, ptr(cos), ptr(sin), rope_dim,
+                                     start_pos)
         return q_out

@@ -130,20 +130,20 @@ void or_qk_norm_rope_append(or_manager *m, int32_t layer, const uint16_t *q_tok,
                             const float *gamma_q, uint16_t *q_out, const uint16_t *k_tok,
                             const uint16_t *v_tok, int32_t n_kv_heads, int32_t seq_len, int32_t head_dim,
                             const float *gamma_k, float eps, const float *cos_tab, const float *sin_tab,
-                            int64_t start_pos) {
+                            int32_t rope_dim, int64_t start_pos) {
     size_t nk = (size_t)n_kv_heads * seq_len * head_dim;
     uint16_t *k4 = (uint16_t *)malloc(nk * 2), *kn = (uint16_t *)malloc(nk * 2);
     uint16_t *kr = (uint16_t *)malloc(nk * 2), *v4 = (uint16_t *)malloc(nk * 2);
     or_permute_tok_to_head(k4, k_tok, seq_len, n_kv_heads, head_dim);
     or_permute_tok_to_head(v4, v_tok, seq_len, n_kv_heads, head_dim);
     or_rms_norm(kn, k4, gamma_k, (size_t)n_kv_heads * seq_len, (size_t)head_dim, eps);
-    or_apply_rope(kr, kn, cos_tab, sin_tab, n_kv_heads, seq_len, head_dim, start_pos);
+    or_apply_rope_partial(kr, kn, cos_tab, sin_tab, n_kv_heads, seq_len, head_dim, rope_dim, start_pos);
     if (q_tok && q_out) {
         size_t nq = (size_t)n_q_heads * seq_len * head_dim;
         uint16_t *q4 = (uint16_t *)malloc(nq * 2), *qn = (uint16_t *)malloc(nq * 2);
         or_permute_tok_to_head(q4, q_tok, seq_len, n_q_heads, head_dim);
         or_rms_norm(qn, q4, gamma_q, (size_t)n_q_heads * seq_len, (size_t)head_dim, eps);
-        or_apply_rope(q_out, qn, cos_tab, sin_tab, n_q_heads, seq_len, head_dim, start_pos);
+        or_apply_rope_partial(q_out, qn, cos_tab, sin_tab, n_q_heads, seq_len, head_dim, rope_dim, start_pos);
         free(q4);
         free(qn);
     }

@@ -17,7 +17,11 @@
  *   block pool / mgr  test_page_attention.cpp (all 5 tests) + LIFO/overflow
  *   rms_norm          test_ops_cpu.cpp:118-148 values + fp64 closed form
  *   rope_cache        fp64 closed form (numpy), bit-exact
- *   apply_rope        pos-0 identity, fp64 closed form, rotation composition
+ *   apply_rope        pos-0 identity, fp64 closed form, rotation composition;
+ *                     the partial form: equal to apply_rope at rope_dim ==
+ *                     head_dim, copied dims bit-exact, fp64 closed form
+ *   linear            integer closed form on every summation path, hand-derived
+ *                     block/tree order cases, fp64 bound
  *   append (scatter)  closed-form page address, bit-exact
  *   paged attention   fp64 brute force, N=1 identity, equal-keys mean,
  *                     dominant-score selection, GQA head map
@@ -96,6 +100,12 @@ void or_rope_cache(float *dst, float theta, int head_dim, int max_seq, int is_co
 /* ---- ApplyRopeImpl<CPU> (bf16): src/backend/cpu/rope.cpp:76-119, B == 1 ---- */
 void or_apply_rope(uint16_t *out, const uint16_t *x, const float *cos_tab, const float *sin_tab,
                    int64_t n_heads, int64_t seq_len, int64_t head_dim, int64_t start_pos);
+/* Partial rotation over the first rope_dim dims with [max_seq][rope_dim]
+ * tables (Qwen3.5, Qwen35.hpp:14-16); the other dims are copied.  No reference
+ * behaviour exists for rope_dim < head_dim (see rope.c); rope_dim == head_dim
+ * is or_apply_rope. */
+void or_apply_rope_partial(uint16_t *out, const uint16_t *x, const float *cos_tab, const float *sin_tab,
+                           int64_t n_heads, int64_t seq_len, int64_t head_dim, int64_t rope_dim, int64_t start_pos);
 
 /* ---- PermuteImpl<CPU> fast path for [1,S,H,D] -> [1,H,S,D]: shape.cpp:69-117 ---- */
 void or_permute_tok_to_head(uint16_t *dst, const uint16_t *src, int64_t S, int64_t H, int64_t D);
@@ -121,12 +131,14 @@ void or_flash_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
 /* ---- Composition used by the Qwen3 layer (Qwen3.cpp:137-166) for the K/V side:
  * token-major k,v [S][Hkv][D] -> permute -> rms_norm(k) -> apply_rope(k) ->
  * append_kv_from_tensor.  Also q (optional, q_out head-major [Hq][S][D]).
- * start_pos is the RoPE op_params[2] (executor.cpp:208-247). */
+ * start_pos is the RoPE op_params[2] (executor.cpp:208-247); rope_dim the
+ * rotated dims (head_dim for Qwen3; 64 of 256 for Qwen3.5's layer,
+ * Qwen35.cpp:191-226). */
 void or_qk_norm_rope_append(or_manager *m, int32_t layer, const uint16_t *q_tok, int32_t n_q_heads,
                             const float *gamma_q, uint16_t *q_out, const uint16_t *k_tok,
                             const uint16_t *v_tok, int32_t n_kv_heads, int32_t seq_len, int32_t head_dim,
                             const float *gamma_k, float eps, const float *cos_tab, const float *sin_tab,
-                            int64_t start_pos);
+                            int32_t rope_dim, int64_t start_pos);
 
 /* ---- linear<bfloat16_t>: src/backend/cpu/linear.cpp:46-122 (LinearImpl<CPU>, :325-345) ----
  * x [rows][common], w [cols][common] (transpose_w = 1), bias [cols] or NULL,

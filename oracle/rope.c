@@ -61,6 +61,42 @@ void or_apply_rope(uint16_t *out, const uint16_t *x, const float *cos_tab, const
     }
 }
 
+/* Partial rotation (Qwen3.5: rope_dimension_count 64 of head_dim 256,
+ * Qwen35.hpp:14-16, tables built by rope_cache(max_seq, 64, theta),
+ * Qwen35.cpp:95-100, so rows of rope_dim floats).  The reference's
+ * ApplyRopeImpl reads op_params[0] only (rope.cpp:80-82) and indexes the
+ * rope_dim-wide table with stride head_dim -- outside the table for this shape
+ * -- so there is no reference behaviour to restate; the op's contract
+ * (op_params[1] = rope_dim = the table width, op_factory.hpp:504-529) and the
+ * Qwen3.5 convention define it: the first rope_dim dims rotate exactly as
+ * or_apply_rope does with head_dim = rope_dim (same expressions, same
+ * contraction), the remaining dims are copied unchanged.  With rope_dim ==
+ * head_dim this is or_apply_rope. */
+void or_apply_rope_partial(uint16_t *out, const uint16_t *x, const float *cos_tab, const float *sin_tab,
+                           int64_t n_heads, int64_t seq_len, int64_t head_dim, int64_t rope_dim, int64_t start_pos) {
+    int64_t half = rope_dim / 2;
+    size_t head_stride = (size_t)(seq_len * head_dim);
+    for (int64_t h = 0; h < n_heads; ++h) {
+        for (int64_t s = 0; s < seq_len; ++s) {
+            int64_t pos = start_pos + s;
+            const float *c = cos_tab + pos * rope_dim;
+            const float *sn = sin_tab + pos * rope_dim;
+            uint16_t *ro = out + (size_t)h * head_stride + (size_t)(s * head_dim);
+            const uint16_t *ri = x + (size_t)h * head_stride + (size_t)(s * head_dim);
+            for (int64_t i = 0; i < half; ++i) {
+                float x0 = or_bf16_to_f32(ri[i]);
+                float x1 = or_bf16_to_f32(ri[i + half]);
+                float ci = c[i], si = sn[i];
+                float xr = x0 * ci - x1 * si;
+                float xi = x0 * si + x1 * ci;
+                ro[i] = or_f32_to_bf16(xr);
+                ro[i + half] = or_f32_to_bf16(xi);
+            }
+            for (int64_t i = rope_dim; i < head_dim; ++i) ro[i] = ri[i];
+        }
+    }
+}
+
 /* PermuteImpl<CPU> fast path (shape.cpp:69-100): the innermost dim is kept, so
  * rows of D elements are copied; here the two permutations the Qwen3 layer uses
  * between [1,S,H,D] and [1,H,S,D] (Qwen3.cpp:137-141, :169). */

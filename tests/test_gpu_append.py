@@ -86,8 +86,9 @@ def test_kv_scatter_bit_exact():
     assert np.array_equal(kh, want_k) and np.array_equal(vh, want_v)
 
 
-def _append_case(orc, S, Hkv, D, pool, start_tokens, seed, with_q=False, Hq=32, head_major=False):
-    cos, sin = paged.rope_cache(1e6, D, start_tokens + S + 1)
+def _append_case(orc, S, Hkv, D, pool, start_tokens, seed, with_q=False, Hq=32, head_major=False, rope_dim=None,
+                 theta=1e6):
+    cos, sin = paged.rope_cache(theta, rope_dim or D, start_tokens + S + 1)
     k = synth.normal_bf16(seed, (S, Hkv, D))
     v = synth.normal_bf16(seed, (S, Hkv, D), offset=1 << 26)
     gk = synth.uniform_f32(seed + 1, (D,), 0.5, 1.5)
@@ -157,3 +158,26 @@ def test_fused_append_ragged_and_head_major(orc, S, start):
 @pytest.mark.parametrize("D,Hkv", [(64, 4), (256, 2), (128, 3)])
 def test_fused_append_other_shapes(orc, D, Hkv):
     _append_case(orc, 45, Hkv, D, 8, 7, 123 + D, with_q=True, Hq=2 * Hkv)
+
+
+@pytest.mark.parametrize("S,start", [(45, 7), (1, 300)])
+def test_fused_append_qwen35_partial_rotary(orc, S, start):
+    """Qwen3.5 attention layer (Qwen35.cpp:191-226): head_dim 256, 8 q / 2 kv
+    heads, RoPE on the first 64 dims (rope_dimension_count, Qwen35.hpp:14-16,
+    theta 1e7), the other 192 passed through after the norm."""
+    _append_case(orc, S, 2, 256, 40, start, 350 + S, with_q=True, Hq=8, rope_dim=64, theta=1e7)
+
+
+def test_fused_append_partial_rotary_d128(orc):
+    _append_case(orc, 33, 8, 128, 8, 3, 360, with_q=True, Hq=16, rope_dim=64)
+
+
+@pytest.mark.parametrize("D,rope_dim", [(256, 64), (256, 128), (128, 64), (256, 256)])
+def test_apply_rope_partial_bit_exact(orc, D, rope_dim):
+    H, S, start = 5, 19, 11
+    cos, sin = paged.rope_cache(1e7, rope_dim, start + S)
+    x = synth.normal_bf16(40 + D + rope_dim, (H, S, D))
+    out = torch.empty((H, S, D), dtype=torch.bfloat16, device="cuda")
+    paged.apply_rope(out, dev(x), torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda(), start)
+    torch.cuda.synchronize()
+    assert np.array_equal(paged.to_host_bits(out), orc.apply_rope_partial(x, cos, sin, start))

@@ -505,3 +505,35 @@ def test_linear_fp64_bound(orc):
     mag = np.abs(xf) @ np.abs(wf).T
     # one bf16 rounding plus fp32 accumulation error (well under common * 2^-24 * mag)
     assert np.all(np.abs(got - exact) <= bf16_ulp(exact) / 2 + common * 2.0 ** -24 * mag)
+
+
+# ------------------------------------------------- partial rotary (Qwen3.5)
+def test_apply_rope_partial_full_width_is_apply_rope(orc):
+    D = 128
+    cos, sin = orc.rope_cache(1e6, D, 32)
+    x = synth.normal_bf16(23, (3, 20, D))
+    assert np.array_equal(orc.apply_rope_partial(x, cos, sin, 7), orc.apply_rope(x, cos, sin, 7))
+
+
+@pytest.mark.parametrize("D,rope_dim", [(256, 64), (256, 128), (128, 64)])
+def test_apply_rope_partial_closed_form(orc, D, rope_dim):
+    S, start = 16, 9
+    cos, sin = orc.rope_cache(1e7, rope_dim, start + S)
+    x = synth.normal_bf16(24 + D + rope_dim, (4, S, D))
+    got = orc.apply_rope_partial(x, cos, sin, start)
+    # dims past rope_dim are copied bit for bit
+    assert np.array_equal(got[..., rope_dim:], x[..., rope_dim:])
+    # the rotated block is the fp64 rotation with rope_dim as the table width
+    half = rope_dim // 2
+    xd = f32(x).astype(np.float64)
+    pos = start + np.arange(S)[None, :, None]
+    ang = pos * np.array([1e7 ** (-2.0 * i / rope_dim) for i in range(half)])[None, None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    x0, x1 = xd[..., :half], xd[..., half:rope_dim]
+    want = np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
+    g = f32(got[..., :rope_dim]).astype(np.float64)
+    assert np.all(np.abs(g - want) <= bf16_ulp(want) * 0.6 + 1e-6)
+    # position 0 rotates by nothing
+    x1pos = x[:, :1]
+    x1pos = np.where((x1pos & 0x7FFF) == 0, np.uint16(0x3F80), x1pos)
+    assert np.array_equal(orc.apply_rope_partial(np.ascontiguousarray(x1pos), cos, sin, 0), x1pos)
