@@ -223,7 +223,8 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) &
 int check_attn_args(const AttnParams& p, int head_dim) {
     if (!p.q || !p.out || !p.k_pool || !p.v_pool || !p.k_ids || !p.v_ids)
         return fail(GENLLM_ERR_INVALID, "paged attention: null pointer");
-    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged attention requires head_dim == 128");
+    if (head_dim != 128 && head_dim != 256)
+        return fail(GENLLM_ERR_UNSUPPORTED, "paged attention requires head_dim 128 or 256");
     if (p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv != 0)
         return fail(GENLLM_ERR_INVALID, "paged attention: n_q_heads must be a multiple of n_kv_heads");
     if (p.S <= 0 || p.n_cached < p.S || p.n_pages < (p.n_cached + kPage - 1) / kPage)
@@ -452,7 +453,8 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     if (!kv) return fail(GENLLM_ERR_INVALID, "paged_attention: null kv");
     LayerState* s = active_layer(kv, layer);
     if (!s) return GENLLM_OK;  // attention.cpp:127: inactive layer, nothing written
-    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention requires head_dim == 128");
+    if (head_dim != 128 && head_dim != 256)
+        return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention requires head_dim 128 or 256");
     if (batch != 1) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention: batch must be 1");
     if (s->dtype != GENLLM_DTYPE_BF16 || s->head_dim != head_dim || s->n_kv_heads != n_kv_heads)
         return fail(GENLLM_ERR_INVALID, "paged_attention: tensor shape/dtype differs from the layer's pools");

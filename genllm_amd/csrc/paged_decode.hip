@@ -48,7 +48,10 @@ constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
 constexpr int kWaves = 4;       // waves of a split workgroup
 constexpr int kMergeWaves = 4;  // waves of a merge workgroup
 constexpr int kMaxSplits = 256;
-constexpr int PF = 3;          // pages in flight per wave (3: two waves per SIMD fit)
+// pages in flight per wave: 3 at D = 128 (two waves per SIMD fit), 2 at
+// D = 256 (a page then takes twice the registers)
+template <int D>
+constexpr int kPagesInFlight = D == 128 ? 3 : 2;
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -62,16 +65,19 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
     return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
 }
 
+template <int D>
 struct PageRegs {
-    uint4 k[4];  // K^T operand chunks (D = 128)
-    uint4 v[4];  // V rows of tokens 4g..4g+3
+    uint4 k[D / 32];       // K^T operand chunks
+    uint4 v[4][D / 128];   // V rows of tokens 4g..4g+3, dims 8 n16 + 128 hh
 };
 
 template <int D>
 __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p) {
-    static_assert(D == 128, "decode kernel: head_dim 128");
-    constexpr int KS = D / 32;  // S^T k-steps
-    constexpr int DB = D / 16;  // O^T dim blocks
+    static_assert(D == 128 || D == 256, "decode kernel: head_dim 128 or 256");
+    constexpr int KS = D / 32;   // S^T k-steps
+    constexpr int DB = D / 16;   // O^T dim blocks
+    constexpr int VH = D / 128;  // 128-dim halves of a V row per lane
+    constexpr int PF = kPagesInFlight<D>;
 
     __shared__ __attribute__((aligned(16))) uint16_t lds_vt[kWaves][D * VT_ROW];
     __shared__ float lds_m[kWaves][kRows], lds_l[kWaves][kRows];
@@ -134,7 +140,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
     auto page_of = [&](int j) { return begin + wv + kWaves * j; };
 
     // Token t >= new_from is this call's append: read it from k_new / v_new.
-    auto load_page = [&](int j, PageRegs& pr, bool special) {
+    auto load_page = [&](int j, PageRegs<D>& pr, bool special) {
         const int pg = page_of(j);
         const uint16_t* kb = p.k_pool + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
         const uint16_t* vb = p.v_pool + int64_t(__builtin_amdgcn_readlane(my_vid, j)) * p.page_elems;
@@ -149,7 +155,10 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
                 pr.k[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, kcol_b + 64 * c, 0, 0));
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                pr.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vcol_b, i * kv_row_b, 0));
+#pragma unroll
+                for (int hh = 0; hh < VH; ++hh)
+                    pr.v[i][hh] = __builtin_bit_cast(
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vcol_b + 256 * hh, i * kv_row_b, 0));
             return;
         }
         const uint16_t* kr = kb + kcol;
@@ -168,11 +177,12 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
                 if (tv >= p.new_from && tv < p.n_cached)
                     src = p.v_new + h * p.new_head_stride + int64_t(tv - p.new_from) * p.new_tok_stride + 8 * n16;
             }
-            pr.v[i] = *reinterpret_cast<const uint4*>(src);
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh) pr.v[i][hh] = *reinterpret_cast<const uint4*>(src + 128 * hh);
         }
     };
     // ... and write the appended rows into their page slots (bit-exact copies)
-    auto store_new = [&](int j, const PageRegs& pr) {
+    auto store_new = [&](int j, const PageRegs<D>& pr) {
         const int pg = page_of(j);
         if (pg * kPage + kPage <= p.new_from) return;  // wave-uniform: no new token in this page
         uint16_t* kb = p.k_pool_w + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
@@ -186,7 +196,8 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
         for (int i = 0; i < 4; ++i) {
             const int tv = pg * kPage + 4 * g + i;
             if (tv >= p.new_from && tv < p.n_cached)
-                *reinterpret_cast<uint4*>(vb + i * p.kv_row + vcol) = pr.v[i];
+#pragma unroll
+                for (int hh = 0; hh < VH; ++hh) *reinterpret_cast<uint4*>(vb + i * p.kv_row + vcol + 128 * hh) = pr.v[i][hh];
         }
     };
 
@@ -195,25 +206,29 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute_page = [&](int j, const PageRegs& pr, bool special) {
+    auto compute_page = [&](int j, const PageRegs<D>& pr, bool special) {
         const int tok0 = page_of(j) * kPage + 4 * g;  // this lane's 4 keys: tok0 .. tok0+3
         // V^T into LDS first (its latency hides behind the S^T MFMAs)
-        uint4 v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = pr.v[i];
-            if (special && tok0 + i >= p.n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots
-        }
-        const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
-                                  {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
+        for (int hh = 0; hh < VH; ++hh) {
+            uint4 v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {  // dims 8*n16 + 2e (low halves) and + 2e + 1 (high halves)
-            const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][e], w[0][e], 0x05040100u),
-                                        __builtin_amdgcn_perm(w[3][e], w[2][e], 0x05040100u));
-            const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][e], w[0][e], 0x07060302u),
-                                        __builtin_amdgcn_perm(w[3][e], w[2][e], 0x07060302u));
-            *reinterpret_cast<uint2*>(&vt[(8 * n16 + 2 * e) * VT_ROW + 4 * g]) = lo;
-            *reinterpret_cast<uint2*>(&vt[(8 * n16 + 2 * e + 1) * VT_ROW + 4 * g]) = hi;
+            for (int i = 0; i < 4; ++i) {
+                v[i] = pr.v[i][hh];
+                if (special && tok0 + i >= p.n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots
+            }
+            const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
+                                      {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
+            const int d0 = 128 * hh + 8 * n16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // dims d0 + 2e (low halves) and + 2e + 1 (high halves)
+                const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][e], w[0][e], 0x05040100u),
+                                            __builtin_amdgcn_perm(w[3][e], w[2][e], 0x05040100u));
+                const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][e], w[0][e], 0x07060302u),
+                                            __builtin_amdgcn_perm(w[3][e], w[2][e], 0x07060302u));
+                *reinterpret_cast<uint2*>(&vt[(d0 + 2 * e) * VT_ROW + 4 * g]) = lo;
+                *reinterpret_cast<uint2*>(&vt[(d0 + 2 * e + 1) * VT_ROW + 4 * g]) = hi;
+            }
         }
         // S^T = K Q^T
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -263,13 +278,13 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
         __builtin_amdgcn_wave_barrier();
     };
 
-    auto load_any = [&](int j, PageRegs& pr) {
+    auto load_any = [&](int j, PageRegs<D>& pr) {
         if (page_of(j) >= special_from)
             load_page(j, pr, true);
         else
             load_page(j, pr, false);
     };
-    PageRegs buf[PF];
+    PageRegs<D> buf[PF];
 #pragma unroll
     for (int u = 0; u < PF - 1; ++u)
         if (u < np) load_any(u, buf[u]);
@@ -304,30 +319,40 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
     }
     __syncthreads();
 
-    // workgroup merge: wave -> rows ri, ri+4, ...; lane -> dims d2, d2+1
+    // workgroup merge: wave -> rows ri, ri+4, ...; lane -> dims d2, d2+1 of
+    // each 128-dim half
     for (int ri = wv; ri < rows_total; ri += kWaves) {
-        const int d2 = lane * 2;
         float M = -INFINITY;
 #pragma unroll
         for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_m[w2][ri]);
-        float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+        float L = 0.0f, O0[VH], O1[VH];
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh) O0[hh] = O1[hh] = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
             for (int w2 = 0; w2 < kWaves; ++w2) {
                 const float e = exp2_fast(lds_m[w2][ri] - M);
                 L += lds_l[w2][ri] * e;
-                O0 += lds_o[w2][ri][d2] * e;
-                O1 += lds_o[w2][ri][d2 + 1] * e;
+#pragma unroll
+                for (int hh = 0; hh < VH; ++hh) {
+                    O0[hh] += lds_o[w2][ri][128 * hh + 2 * lane] * e;
+                    O1[hh] += lds_o[w2][ri][128 * hh + 2 * lane + 1] * e;
+                }
             }
         }
         if (p.n_splits == 1) {
             uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
             const float inv = 1.0f / L;
-            *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(O0 * inv), f32_to_bf16_ref(O1 * inv));
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh)
+                *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
+                    pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
         } else {
             // partials: o [h][split][row][D], then {m, l} [h][split][row]
             float* po = p.partial + ((int64_t(h) * p.n_splits + sp) * rows_total + ri) * D;
-            *reinterpret_cast<float2*>(po + d2) = make_float2(O0, O1);
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh)
+                *reinterpret_cast<float2*>(po + 128 * hh + 2 * lane) = make_float2(O0[hh], O1[hh]);
             if (lane == 0) {
                 float2* ml = reinterpret_cast<float2*>(p.partial + int64_t(p.Hkv) * p.n_splits * rows_total * D);
                 ml[(int64_t(h) * p.n_splits + sp) * rows_total + ri] = make_float2(M, L);
@@ -344,26 +369,31 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
 //   M = max M_w, L = sum L_w 2^(M_w - M), O = sum O_w 2^(M_w - M), out = O / L.
 template <int D>
 __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_merge_kernel(AttnParams p) {
-    constexpr int U = 16;  // splits in flight per lane
+    constexpr int U = 16;        // splits in flight per lane
+    constexpr int VH = D / 128;  // lane -> dims 128 hh + 2 lane, +1
     __shared__ float s_o[kMergeWaves][D];
     __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int ri = blockIdx.x, h = blockIdx.y;
     const int rows = p.G * p.S;
     const int ns = p.n_splits;  // <= kMaxSplits
-    const int d2 = lane * 2;
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
                        int64_t(h) * ns * rows + ri;
-    const float2* po = reinterpret_cast<const float2*>(p.partial + (int64_t(h) * ns * rows + ri) * D + d2);
-    const int64_t sstride = int64_t(rows) * D / 2;  // float2 units between splits
+    const float* po = p.partial + (int64_t(h) * ns * rows + ri) * D + 2 * lane;
+    const int64_t sstride = int64_t(rows) * D;  // floats between splits
 
-    float mw = -INFINITY, lw = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    float mw = -INFINITY, lw = 0.0f, o0[VH], o1[VH];
+#pragma unroll
+    for (int hh = 0; hh < VH; ++hh) o0[hh] = o1[hh] = 0.0f;
     for (int s0 = wv; s0 < ns; s0 += kMergeWaves * U) {
-        float2 ov[U], mv[U];
+        float2 ov[U][VH], mv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int s2 = s0 + kMergeWaves * u;
-            ov[u] = s2 < ns ? po[s2 * sstride] : make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh)
+                ov[u][hh] = s2 < ns ? *reinterpret_cast<const float2*>(po + s2 * sstride + 128 * hh)
+                                    : make_float2(0.0f, 0.0f);
             mv[u] = s2 < ns ? ml[s2 * rows] : make_float2(-INFINITY, 0.0f);
         }
         float bm = mw;
@@ -372,19 +402,28 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_merge_kernel(At
         if (bm == -INFINITY) continue;  // nothing visible yet
         const float a = mw == -INFINITY ? 0.0f : exp2_fast(mw - bm);
         lw *= a;
-        o0 *= a;
-        o1 *= a;
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh) {
+            o0[hh] *= a;
+            o1[hh] *= a;
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const float w = mv[u].x == -INFINITY ? 0.0f : exp2_fast(mv[u].x - bm);
             lw += mv[u].y * w;
-            o0 += ov[u].x * w;
-            o1 += ov[u].y * w;
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh) {
+                o0[hh] += ov[u][hh].x * w;
+                o1[hh] += ov[u][hh].y * w;
+            }
         }
         mw = bm;
     }
-    s_o[wv][d2] = o0;
-    s_o[wv][d2 + 1] = o1;
+#pragma unroll
+    for (int hh = 0; hh < VH; ++hh) {
+        s_o[wv][128 * hh + 2 * lane] = o0[hh];
+        s_o[wv][128 * hh + 2 * lane + 1] = o1[hh];
+    }
     if (lane == 0) {
         s_m[wv] = mw;
         s_l[wv] = lw;
@@ -394,17 +433,25 @@ __global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_merge_kernel(At
         float M = -INFINITY;
 #pragma unroll
         for (int w2 = 0; w2 < kMergeWaves; ++w2) M = fmaxf(M, s_m[w2]);
-        float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+        float L = 0.0f, O0[VH], O1[VH];
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh) O0[hh] = O1[hh] = 0.0f;
 #pragma unroll
         for (int w2 = 0; w2 < kMergeWaves; ++w2) {
             const float e = s_m[w2] == -INFINITY ? 0.0f : exp2_fast(s_m[w2] - M);
             L += s_l[w2] * e;
-            O0 += s_o[w2][d2] * e;
-            O1 += s_o[w2][d2 + 1] * e;
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh) {
+                O0[hh] += s_o[w2][128 * hh + 2 * lane] * e;
+                O1[hh] += s_o[w2][128 * hh + 2 * lane + 1] * e;
+            }
         }
         const float inv = 1.0f / L;
         uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
-        *reinterpret_cast<uint32_t*>(orow + d2) = pack2(f32_to_bf16_ref(O0 * inv), f32_to_bf16_ref(O1 * inv));
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh)
+            *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
+                pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
     }
 }
 
@@ -446,18 +493,23 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
     return GENLLM_OK;
 }
 
-int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
-    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged decode: head_dim must be 128");
-    if (p.n_pages <= 0) return GENLLM_OK;
-    if (p.n_splits > kMaxSplits || p.pages_per_split > 64 * kWaves || p.G * p.S > kRows)
-        return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
-    hipLaunchKernelGGL(paged_decode_kernel<128>, dim3(p.n_splits, p.Hkv), dim3(kWaves * 64), 0, stream, p);
+template <int D>
+int launch_decode_d(const AttnParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL(paged_decode_kernel<D>, dim3(p.n_splits, p.Hkv), dim3(kWaves * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1) {
-        hipLaunchKernelGGL(paged_decode_merge_kernel<128>, dim3(p.G * p.S, p.Hkv), dim3(kMergeWaves * 64), 0, stream, p);
+        hipLaunchKernelGGL(paged_decode_merge_kernel<D>, dim3(p.G * p.S, p.Hkv), dim3(kMergeWaves * 64), 0, stream, p);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;
+}
+
+int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
+    if (head_dim != 128 && head_dim != 256) return fail(GENLLM_ERR_UNSUPPORTED, "paged decode: head_dim must be 128 or 256");
+    if (p.n_pages <= 0) return GENLLM_OK;
+    if (p.n_splits > kMaxSplits || p.pages_per_split > 64 * kWaves || p.G * p.S > kRows)
+        return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
+    return head_dim == 128 ? launch_decode_d<128>(p, stream) : launch_decode_d<256>(p, stream);
 }
 
 }  // namespace genllm

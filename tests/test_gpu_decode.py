@@ -130,3 +130,25 @@ def test_decode_repeat_is_deterministic(orc):
     b, _ = ctx.decode(q)
     assert np.array_equal(a, b)
     ctx.close()
+
+
+@pytest.mark.parametrize("N,pps", [(1, None), (17, None), (300, None), (4099, None), (1000, 3)])
+def test_decode_qwen35_head_dim_256(orc, N, pps):
+    """Qwen3.5 attention layer shape (Qwen35.hpp:14-16): 8 q heads, 2 kv heads,
+    head_dim 256 (GQA 4:1)."""
+    pool = max(8, (N + 15) // 16 + 3)
+    ctx = Context(orc, 2, 256, pool, N, 3000 + N, nan_tail=True)
+    q = synth.normal_bf16(3100 + N, (8, 1, 256))
+    got, _ = ctx.decode(q, pps=pps)
+    assert_attn_close(got, ctx.oracle(q), f"D256 N{N} pps{pps}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("S,causal", [(2, True), (4, True), (3, False)])
+def test_decode_multi_query_head_dim_256(orc, S, causal):
+    N = 190
+    ctx = Context(orc, 2, 256, 16, N, 3300 + S, nan_tail=True)
+    q = synth.normal_bf16(3400 + S, (8, S, 256))
+    got, _ = ctx.decode(q, causal=causal)
+    assert_attn_close(got, ctx.oracle(q, causal), f"D256 S{S} causal{causal}")
+    ctx.close()

@@ -147,3 +147,25 @@ def test_manager_state_machine_matches_oracle(orc):
     mgr.block_alloc(3, 1)
     assert mgr.block_alloc(3, 1) == -1
     mgr.close()
+
+
+def test_op_qwen35_decode_with_append(orc):
+    """The op at the Qwen3.5 attention shape (head_dim 256, 8 q / 2 kv heads):
+    a warm cache of 150 tokens, then decode steps that append and attend
+    (crossing a page boundary) and a short chunk."""
+    Hq, Hkv, D, pool = 8, 2, 256, 30
+    mgr, ref = make(orc, Hkv, D, pool, 77)
+    mgr.append_kv_pages(0, 150)
+    ref.append_kv_pages(0, 150)
+    kp = synth.normal_bf16(78, (pool, 16, Hkv, D))
+    vp = synth.normal_bf16(79, (pool, 16, Hkv, D))
+    ref.pool_array(0, 0)[:] = kp
+    ref.pool_array(0, 1)[:] = vp
+    mgr.write_pool(0, 0, kp)
+    mgr.write_pool(0, 1, vp)
+    for i in range(12):
+        step(mgr, ref, 0, Hq, Hkv, 1, D, 800 + 10 * i, f"qwen35 decode {151 + i}")
+    step(mgr, ref, 0, Hq, Hkv, 4, D, 990, "qwen35 chunk of 4")
+    assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0))
+    assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1))
+    mgr.close()
