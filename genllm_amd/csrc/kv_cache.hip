@@ -737,7 +737,8 @@ extern "C" int genllm_flash_attention(const void* q, const void* k, const void* 
                                       int32_t n_q_heads, int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
                                       int32_t n_kv_groups, float scale, int32_t causal, void* stream) {
     if (!q || !k || !v || !out) return fail(GENLLM_ERR_INVALID, "flash_attention: null tensor");
-    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "flash_attention requires head_dim == 128");
+    if (head_dim != 128 && head_dim != 256)
+        return fail(GENLLM_ERR_UNSUPPORTED, "flash_attention requires head_dim 128 or 256");
     if (batch < 0 || seq_len < 0 || n_kv_heads <= 0 || n_kv_groups <= 0 || n_q_heads != n_kv_heads * n_kv_groups)
         return fail(GENLLM_ERR_INVALID, "flash_attention: n_q_heads must equal n_kv_heads * n_kv_groups");
     if (!(scale >= 0.0f) || scale == INFINITY)

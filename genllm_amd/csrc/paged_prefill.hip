@@ -403,11 +403,249 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     }
 }
 
+// ---------------------------------------------------------------- D = 256
+// Qwen3.5's head_dim (Qwen35.hpp:14-16).  A token row is 512 B (32 chunks of
+// 16 B); both 256-byte halves carry the swizzle above (chunk c of row r at
+// position 16 (c / 16) + ((c % 16) ^ swz(r % 16))).  Two query blocks per wave
+// would need 128 accumulator registers here, so each wave owns one 16-query
+// block and every key of the tile; key tiles are 32 tokens (2 pages), double
+// buffered in 64 KB of LDS (two workgroups per CU).  Wave w moves the K
+// (w even) or V (w odd) rows of page w / 2 of each tile.
+constexpr int KT256 = 32;
+constexpr int QW256 = 16;
+constexpr int QT256 = QW256 * WAVES;
+
+__global__ __launch_bounds__(WAVES * 64) void paged_prefill_d256_kernel(AttnParams p) {
+    constexpr int D = 256;
+    constexpr int KS = D / 32, DB = D / 16;
+    constexpr int ROWB = D * 2;          // 512 bytes per token row
+    constexpr int TILEB = KT256 * ROWB;  // 16 KB of K (or V) per tile
+    __shared__ __attribute__((aligned(16))) char lds_b0[2 * TILEB];
+    __shared__ __attribute__((aligned(16))) char lds_b1[2 * TILEB];
+    lds_char* const buf0 = (lds_char*)lds_b0;
+    lds_char* const buf1 = (lds_char*)lds_b1;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15, g = lane >> 4;
+    const int n_qt = (p.S + QT256 - 1) / QT256;
+    const int rank = int(blockIdx.x) / p.Hq;
+    const int hq = int(blockIdx.x) - rank * p.Hq;
+    const int heavy = (n_qt + 1) / 2;
+    const int qt = rank < heavy ? n_qt - 1 - rank : rank - heavy;  // heavy and light tiles paired
+    const int hkv = hq / p.G;
+    const int qabs0 = p.n_cached - p.S;
+    const int q0 = qt * QT256 + wv * QW256;
+
+    bf16x8_t qb[KS];
+    {
+        const int s = q0 + n16;
+        const bool ok = s < p.S;
+        const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(ok ? s : p.S - 1) * p.q_tok_stride;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
+            if (!ok) u = make_uint4(0, 0, 0, 0);
+            qb[ks] = as_bf16x8(u);
+        }
+    }
+    float m = -INFINITY, l = 0.0f;
+    f32x4_t acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int wg_last = min(qt * QT256 + QT256, p.S) - 1;
+    const int kv_end = p.causal ? min(qabs0 + wg_last + 1, p.n_cached) : p.n_cached;
+    const int n_tiles = (kv_end + KT256 - 1) / KT256;
+    const bool wave_has_rows = q0 < p.S;
+    const int w_last_abs = qabs0 + min(q0 + QW256, p.S) - 1;
+    const int wave_lim = p.causal ? min(qabs0 + q0 + 1, p.n_cached) : p.n_cached;
+
+    // ---- staging: wave w moves kind w % 2 (K, V) of page w / 2 of each tile;
+    // lanes 0..1 hold the tile's two K ids, lanes 2..3 the V ids
+    const int32_t* const k_ids = p.k_ids;
+    const int32_t* const v_ids = p.v_ids;
+    const bool paged = k_ids != nullptr;
+    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
+    const int kind = wv & 1, pg = wv >> 1;
+    const uint16_t* const src = (kind ? p.v_pool : p.k_pool) + head_off;
+    const int64_t kv_row = p.kv_row, page_elems = p.page_elems;
+    const int n_cached = p.n_cached;
+    auto load_ids = [&](int tile) -> int {
+        const int page = 2 * tile + (lane & 1);
+        int id = 0;
+        if (lane < 4 && page * kPage < kv_end) id = !paged ? page : lane < 2 ? k_ids[page] : v_ids[page];
+        return id;
+    };
+    // instruction e fills rows 2e, 2e+1 of the page: lane -> row 2e + lane/32,
+    // position lane%32 <- chunk 16 (p/16) + ((p%16) ^ swz(row))
+    const int kv_row_bytes = int(kv_row) * 2;
+    uint32_t dma_off[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int row = 2 * e + (lane >> 5), pos = lane & 31;
+        const int chunk = 16 * (pos >> 4) + ((pos & 15) ^ swz(row));
+        dma_off[e] = uint32_t(row * kv_row_bytes + 16 * chunk);
+    }
+    const uint32_t page_span = uint32_t(15 * kv_row_bytes + ROWB);
+    const int dst0 = kind * TILEB + pg * (kPage * ROWB);
+    auto issue_tile = [&](int tile, int ids, lds_char* buf) {
+        const int tok_page = tile * KT256 + kPage * pg;
+        int64_t base;
+        uint32_t span;
+        if (paged) {
+            base = int64_t(__builtin_amdgcn_readlane(ids, 2 * kind + pg)) * page_elems;
+            span = page_span;
+        } else {
+            base = int64_t(tok_page) * kv_row;
+            span = uint32_t(__builtin_amdgcn_readfirstlane(max(min(n_cached - tok_page, kPage), 0) * kv_row_bytes));
+        }
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), 0, span, kBufferFlags);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(buf + (dst0 + e * 1024)),
+                                                     16, dma_off[e], 0, 0, 0);
+    };
+    // V rows at or past kv_end are zeroed by the wave that loaded them
+    auto clear_tail = [&](int tile, lds_char* buf) {
+        if (kind == 0) return;
+        const int first = tile * KT256 + kPage * pg;
+        if (first + kPage <= kv_end) return;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int row = 2 * e + (lane >> 5);
+            if (first + row >= kv_end)
+                *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(buf + (dst0 + e * 1024 + 16 * lane)) =
+                    u32x4_t{0u, 0u, 0u, 0u};
+        }
+    };
+
+    auto compute_tile = [&](int t, const lds_char* buf, bool masked) {
+        const int tok0 = t * KT256;
+        f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int row = 16 * kb + n16;
+                const int pos = 16 * (ks >> 2) + ((4 * (ks & 3) + g) ^ swz(n16));
+                const u32x4_t a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+                    buf + (row * ROWB + pos * 16));
+                s[kb] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[ks], s[kb]);
+            }
+        const float c = fmaxf(p.scale_log2, __FLT_MIN__);  // > 0: masked -inf scores give exactly 0
+        if (masked) {
+            __asm__ volatile("");  // keep a branch: full tiles carry no selects
+            const int qpos = qabs0 + q0 + n16;
+            const int lim = p.causal ? min(qpos + 1, n_cached) : n_cached;
+            const int rel = lim - tok0 - 4 * g;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[kb][i] = (16 * kb + i < rel) ? s[kb][i] : -INFINITY;
+        }
+        float mr = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mr = fmaxf(mr, s[kb][i]);
+        float mx = mr * c;
+        if (__any(mx > m + 8.0f)) {  // lazy rescale, as in the D = 128 kernel
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool grow = mx > m + 8.0f;
+            const float mn = grow ? mx : m;
+            const float alpha = grow ? exp2_fast(m - mn) : 1.0f;
+            l *= alpha;
+            m = mn;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+        }
+        const float mu = m == -INFINITY ? 0.0f : m;
+        float sum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = exp2_fast(__builtin_fmaf(s[kb][i], c, -mu));
+                s[kb][i] = e;
+                sum += e;
+            }
+        l += sum;
+        uint4 u;
+        u.x = bf16_pair_rne(s[0][0], s[0][1]);
+        u.y = bf16_pair_rne(s[0][2], s[0][3]);
+        u.z = bf16_pair_rne(s[1][0], s[1][1]);
+        u.w = bf16_pair_rne(s[1][2], s[1][3]);
+        const bf16x8_t pb = as_bf16x8(u);
+        // V^T from two transposing reads per 16 dims: rows 4g + n16/4 and + 16,
+        // dims 16db + 4(n16%4)..+3 (chunk 2db + (n16%4)/2, half n16%2); one
+        // integer offset per read (see the D = 128 kernel)
+        const int row0 = 4 * g + (n16 >> 2), row1 = row0 + 16;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int chunk = 2 * db + ((n16 & 3) >> 1), half = (n16 & 1) * 8;
+            const int pos = 16 * (chunk >> 4) + ((chunk & 15) ^ swz(row0 & 15));
+            const int off0 = TILEB + row0 * ROWB + pos * 16 + half;
+            const int off1 = TILEB + row1 * ROWB + pos * 16 + half;  // row1 % 16 == row0 % 16
+            const s16x4_t lo = ds_read_tr(buf + off0);
+            const s16x4_t hi = ds_read_tr(buf + off1);
+            const s16x4_t a8[2] = {lo, hi};
+            acc[db] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a8), pb, acc[db]);
+        }
+    };
+
+    int ids_next = 0;
+    if (n_tiles > 0) {
+        const int ids0 = load_ids(0);
+        if (n_tiles > 1) ids_next = load_ids(1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        issue_tile(0, ids0, buf0);
+    }
+    auto step = [&](int t, lds_char* cur, lds_char* nxt) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        clear_tail(t, cur);
+        __syncthreads();
+        if (t + 1 < n_tiles) {
+            issue_tile(t + 1, ids_next, nxt);
+            if (t + 2 < n_tiles) ids_next = load_ids(t + 2);
+        }
+        const int tok0 = t * KT256;
+        if (wave_has_rows && !(p.causal && tok0 > w_last_abs)) compute_tile(t, cur, tok0 + KT256 > wave_lim);
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        step(t, buf0, buf1);
+        if (t + 1 < n_tiles) step(t + 1, buf1, buf0);
+    }
+
+    if (!wave_has_rows) return;
+    float lt = l;
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const float inv = 1.0f / lt;
+    const int s = q0 + n16;
+    if (s >= p.S) return;
+    uint16_t* orow = p.out + int64_t(hq) * p.o_head_stride + int64_t(s) * p.o_tok_stride;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        uint2 w;
+        w.x = pack2(f32_to_bf16_ref(acc[db][0] * inv), f32_to_bf16_ref(acc[db][1] * inv));
+        w.y = pack2(f32_to_bf16_ref(acc[db][2] * inv), f32_to_bf16_ref(acc[db][3] * inv));
+        *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = w;
+    }
+}
+
 }  // namespace
 
 int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream) {
-    if (head_dim != 128) return fail(GENLLM_ERR_UNSUPPORTED, "paged prefill: head_dim must be 128");
+    if (head_dim != 128 && head_dim != 256) return fail(GENLLM_ERR_UNSUPPORTED, "paged prefill: head_dim must be 128 or 256");
     if (p.S <= 0 || p.n_pages <= 0) return GENLLM_OK;
+    if (head_dim == 256) {
+        const int64_t n_qt = (p.S + QT256 - 1) / QT256;
+        hipLaunchKernelGGL(paged_prefill_d256_kernel, dim3(unsigned(n_qt * p.Hq)), dim3(WAVES * 64), 0, stream, p);
+        GENLLM_LAUNCH_CHECK("paged_prefill_d256_kernel");
+        return GENLLM_OK;
+    }
     const int64_t n_qt = (p.S + QT - 1) / QT;
     hipLaunchKernelGGL(paged_prefill_kernel<128>, dim3(unsigned(n_qt * p.Hq)), dim3(WAVES * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_prefill_kernel");

@@ -109,9 +109,11 @@ int genllm_kv_block_free(genllm_kv *kv, int32_t layer, int32_t which, int32_t id
  * pages, then attend.  q, out: head-major [batch=1][n_q_heads][seq_len][head_dim];
  * k, v: [1][n_kv_heads][seq_len][head_dim] (op_factory.hpp:413-476).  scale,
  * causal and n_kv_groups are op_params[1..3].  An inactive layer returns
- * GENLLM_OK without touching out (attention.cpp:127).  head_dim != 128 returns
- * GENLLM_ERR_UNSUPPORTED (attention.cu:511).  seq_len == 1 runs the split-K
- * decode kernel, longer chunks the MFMA prefill kernel. */
+ * GENLLM_OK without touching out (attention.cpp:127).  head_dim 128 (Qwen3)
+ * and 256 (Qwen3.5, Qwen35.hpp:14-16) are served; any other returns
+ * GENLLM_ERR_UNSUPPORTED (the CUDA op throws for head_dim != 128,
+ * attention.cu:511).  Chunks of up to 16 (query, q-head) rows per kv head run
+ * the split-K decode kernel, longer chunks the MFMA prefill kernel. */
 int genllm_paged_attention(genllm_kv *kv, int32_t layer, const void *q, const void *k, const void *v, void *out,
                            int32_t batch, int32_t n_q_heads, int32_t seq_len, int32_t head_dim,
                            int32_t n_kv_heads, int32_t n_kv_groups, float scale, int32_t causal, void *stream);
@@ -195,7 +197,7 @@ int genllm_paged_prefill(const void *q, int64_t q_head_stride, int64_t q_tok_str
  * no cache (the op type of kv_cache_per_layer = 0, README.md:97).  q, out:
  * [batch][n_q_heads][seq_len][head_dim]; k, v: [batch][n_kv_heads][seq_len][head_dim],
  * contiguous bf16.  kv head = q head / n_kv_groups; causal masks key s_kv > s_q.
- * head_dim != 128 returns GENLLM_ERR_UNSUPPORTED. */
+ * head_dim 128 or 256; any other returns GENLLM_ERR_UNSUPPORTED. */
 int genllm_flash_attention(const void *q, const void *k, const void *v, void *out, int32_t batch,
                            int32_t n_q_heads, int32_t seq_len, int32_t n_kv_heads, int32_t head_dim,
                            int32_t n_kv_groups, float scale, int32_t causal, void *stream);

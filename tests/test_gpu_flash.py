@@ -74,6 +74,24 @@ def test_flash_prefill_size_vs_torch():
         assert_attn_close(paged.to_host_bits(out[0, h]), want, f"flash 2048 head {h}")
 
 
+@pytest.mark.parametrize("S,causal", [(77, True), (200, False), (1, True)])
+def test_flash_head_dim_256_vs_oracle(orc, S, causal):
+    """Qwen3.5 attention shape (head_dim 256, 8 q / 2 kv heads) without paging."""
+    import torch
+
+    from genllm_amd import paged, synth
+
+    B, Hq, Hkv, D = 1, 8, 2, 256
+    scale = 1.0 / np.sqrt(D)
+    q, k, v = _inputs(synth, 950 + S, B, Hq, Hkv, S, D)
+    out = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    paged.flash_attention(paged.to_device_bf16(q), paged.to_device_bf16(k), paged.to_device_bf16(v), out,
+                          Hq // Hkv, scale, causal)
+    torch.cuda.synchronize()
+    assert_attn_close(paged.to_host_bits(out), orc.flash_attention(q, k, v, Hq // Hkv, scale, causal),
+                      f"flash D256 S{S}")
+
+
 def test_flash_rejects_bad_shapes():
     import torch
 

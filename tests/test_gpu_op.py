@@ -169,3 +169,18 @@ def test_op_qwen35_decode_with_append(orc):
     assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0))
     assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1))
     mgr.close()
+
+
+def test_op_qwen35_prefill_decode_sequence(orc):
+    """The op at the Qwen3.5 shape through every kernel: a 70-token prefill (the
+    D = 256 MFMA prefill), decode steps (split-K decode with the append fused)
+    and a 40-token chunk on the warm cache."""
+    Hq, Hkv, D, pool = 8, 2, 256, 16
+    mgr, ref = make(orc, Hkv, D, pool, 91)
+    step(mgr, ref, 0, Hq, Hkv, 70, D, 1200, "qwen35 prefill 70")
+    for i in range(5):
+        step(mgr, ref, 0, Hq, Hkv, 1, D, 1300 + 10 * i, f"qwen35 decode {71 + i}")
+    step(mgr, ref, 0, Hq, Hkv, 40, D, 1400, "qwen35 chunk 40")
+    assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0))
+    assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1))
+    mgr.close()

@@ -90,3 +90,34 @@ def test_prefill_config4(orc):
     assert rc == 0
     assert_attn_close(got_h[:G], o[0], "config4 heads 0-1 vs oracle")
     ctx.close()
+
+
+@pytest.mark.parametrize("S,N,causal", [
+    (64, 64, True),
+    (300, 300, True),     # ragged query tile and page
+    (200, 333, True),     # chunked prefill: 133 tokens already cached
+    (129, 129, False),
+    (17, 40, True),
+])
+def test_prefill_head_dim_256_vs_oracle(orc, S, N, causal):
+    """Qwen3.5 attention layer (Qwen35.cpp:191-226): head_dim 256, 8 q heads
+    over 2 kv heads, the D = 256 prefill kernel."""
+    Hq, Hkv, D = 8, 2, 256
+    pool = (N + 15) // 16 + 5
+    ctx = Context(orc, Hkv, D, pool, N, 5000 + S + N, nan_tail=True)
+    q = synth.normal_bf16(5100 + S, (Hq, S, D))
+    got = run_prefill(ctx, q, causal)
+    assert_attn_close(got, ctx.oracle(q, causal), f"prefill D256 S{S} N{N} causal{causal}")
+    ctx.close()
+
+
+def test_prefill_head_dim_256_long_vs_torch(orc):
+    """2048-token Qwen3.5-shape causal prefill against float32 torch (all heads)."""
+    Hq, Hkv, S, D = 8, 2, 2048, 256
+    ctx = Context(orc, Hkv, D, 128, S, 5500)
+    q = synth.normal_bf16(5501, (Hq, S, D))
+    got = run_prefill(ctx, q, True)
+    ref = torch_reference(ctx, q, range(Hq))
+    want = synth.f32_to_bf16_bits(np.stack([ref[h] for h in range(Hq)]).astype(np.float32))
+    assert_attn_close(got, want, "prefill D256 2048 vs torch fp32")
+    ctx.close()
