@@ -108,6 +108,12 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const bf16x8_t& a, const bf16x8_
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));  // 16x16x16 MFMA A/B operand (4 bf16)
+
+__device__ __forceinline__ f32x4_t mfma16x16x16(const s16x4_t& a, const s16x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
 // Host helpers
 int device_cu_count();
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

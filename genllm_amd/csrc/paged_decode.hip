@@ -54,12 +54,6 @@ template <int D>
 constexpr int kPagesInFlight = D == 128 ? 3 : 2;
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
 
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f32x4_t mfma16x16x16(const s16x4_t& a, const s16x4_t& b, const f32x4_t& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-
 __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
     const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
     return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);

@@ -32,7 +32,6 @@ __global__ void fill_normal_kernel(uint16_t* dst, size_t n, uint64_t seed, uint6
 // (v_mfma_f32_16x16x32_bf16) or K = 16 (v_mfma_f32_16x16x16_bf16):
 // lane l gives A[l%16][kk(l/16)..+kk-1] and B[kk(l/16)..+kk-1][l%16] with
 // kk = K/4; D[4(l/16)+i][l%16] comes back in register i.
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 __global__ void selftest_mfma_kernel(const uint16_t* a, const uint16_t* b, float* c, int K) {
     const int l = threadIdx.x;
