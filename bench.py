@@ -14,13 +14,16 @@ dominant kernel (paged_decode_kernel + its split merge) timed alone with HIP
 events around each launch on the launch stream, against 8 TB/s; its HBM
 traffic comes from the committed rocprofv3 --pmc summary when present.
 Secondary figures (same line): config 2 fused append GB/s, config 4 causal
-prefill TFLOPS, config 5 36-layer long-context decode (eager and replayed as
-one HIP graph), and the Qwen3-4B fused Q/K/V projection feeding the path (decode
-GEMV GB/s, 2048-token GEMM TFLOPS).  cpu_baseline = the oracle (single
-thread) on a bounded sample of the headline workload.
+prefill TFLOPS, the non-paged FlashAttention path at config 4's shape, the
+Qwen3.5 shape (head_dim 256, 8 q / 2 kv heads: 8K-context decode GB/s and
+2048-token prefill TFLOPS), config 5 36-layer long-context decode (eager and
+replayed as one HIP graph), and the Qwen3-4B fused Q/K/V projection feeding
+the path (decode GEMV GB/s, 2048-token GEMM TFLOPS).  cpu_baseline = the
+oracle (single thread) on a bounded sample of the headline workload.
 
---only {headline,append,prefill,longctx,linear,copy} runs one workload alone
-(for rocprofv3 passes); the line then carries only that workload's figures.
+--only {headline,append,prefill,flash,qwen35,longctx,linear,copy} runs one
+workload alone (for rocprofv3 passes); the line then carries only that
+workload's figures.
 """
 from __future__ import annotations
 
@@ -48,7 +51,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
-    ap.add_argument("--only", choices=["headline", "append", "prefill", "longctx", "linear", "copy"], default=None)
+    ap.add_argument("--only", choices=["headline", "append", "prefill", "flash", "qwen35", "longctx", "linear", "copy"],
+                    default=None)
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -246,6 +250,103 @@ def prefill_cfg4(np, torch, paged, synth, call, iters=40):
             "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}
 
 
+def flash_cfg4(np, torch, paged, synth, call, iters=40):
+    """FlashAttentionImpl (attention.cpp:39-121, the kv_cache_per_layer = 0
+    branch) at config 4's shape: q, out [1,16,2048,128] and k, v [1,8,2048,128]
+    contiguous head-major, causal -- the prefill kernel with identity pages."""
+    Hq, Hkv, D, S = 16, 8, 128, 2048
+    seed = synth.config_seed(4)
+    copies = 4
+    qs, ks, vs = [], [], []
+    for c in range(copies):
+        q = torch.empty((1, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+        k = torch.empty((1, Hkv, S, D), dtype=torch.bfloat16, device="cuda")
+        v = torch.empty_like(k)
+        paged.fill_normal_bf16(q, seed + 60 + c)
+        paged.fill_normal_bf16(k, seed + 70 + c)
+        paged.fill_normal_bf16(v, seed + 80 + c)
+        qs.append(q), ks.append(k), vs.append(v)
+    o = torch.empty((1, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+
+    def run(i):
+        c = i % copies
+        paged.flash_attention(qs[c], ks[c], vs[c], o, Hq // Hkv, 1.0 / np.sqrt(D))
+
+    avg_us, _ = time_launches(torch, run, iters)
+    flops = 4 * D * Hq * S * (S + 1) // 2
+    tfl = flops / (avg_us * 1e-6) / 1e12
+    return {"avg_launch_us": round(avg_us, 3), "flops": flops, "TFLOPS": round(tfl, 1),
+            "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}
+
+
+def qwen35_d256(np, torch, paged, synth, call, iters=100):
+    """The paged op's kernels at Qwen3.5's attention shape (Qwen35.hpp:14-16:
+    head_dim 256, 8 q / 2 kv heads): decode of one query at 8193 cached keys
+    (the split-K decode kernel at D = 256; 16 layers of pools rotate so the
+    MALL cannot serve them) and a causal 2048-token prefill (the D = 256
+    prefill kernel)."""
+    Hq, Hkv, D = 8, 2, 256
+    seed = synth.config_seed(3) + 256
+    pool, n_keys, L = 1024, 8193, 16
+    n_pages = (n_keys + 15) // 16
+    m = paged.PagedAttentionManager(L * (2 * pool * PAGE * Hkv * D * 2 + 8 * pool + 4096) + (1 << 20))
+    for l in range(L):
+        m.init_layer(l, Hkv, D)
+        m.reserve_layer(l, pool)
+        m.fragment(l, synth.shuffled(seed + 2 * l, pool), synth.shuffled(seed + 2 * l + 1, pool))
+        m.append_kv_pages(l, n_keys)
+        inf = m.get_layer(l)
+        call("genllm_fill_normal_bf16", inf.k_pool, pool * PAGE * Hkv * D, seed + 100 + l, 0, None)
+        call("genllm_fill_normal_bf16", inf.v_pool, pool * PAGE * Hkv * D, seed + 200 + l, 0, None)
+    q = torch.empty((L, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    paged.fill_normal_bf16(q, seed + 300)
+    o = torch.empty((Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(paged.decode_workspace_bytes(Hq, Hkv, 1, D, pool), dtype=torch.uint8, device="cuda")
+    infos = [m.get_layer(l) for l in range(L)]
+
+    def dec(i):
+        inf = infos[i % L]
+        paged.paged_decode(q[i % L], o, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, n_pages, n_keys, Hkv,
+                           1.0 / np.sqrt(D), ws)
+
+    d_us, d_ms = time_launches(torch, dec, iters)
+    m.close()
+    d_bytes = decode_kernel_bytes(n_keys, Hq, Hkv, D)
+    d_gbs = d_bytes / (d_us * 1e-6) / 1e9
+
+    S, copies = 2048, 4
+    mp = paged.PagedAttentionManager(copies * (2 * 128 * PAGE * Hkv * D * 2 + 8 * 128 + 4096) + (1 << 20))
+    qs = []
+    for c in range(copies):
+        mp.init_layer(c, Hkv, D)
+        mp.reserve_layer(c, 128)
+        mp.fragment(c, synth.shuffled(seed + 50 + 2 * c, 128), synth.shuffled(seed + 51 + 2 * c, 128))
+        mp.append_kv_pages(c, S)
+        inf = mp.get_layer(c)
+        call("genllm_fill_normal_bf16", inf.k_pool, 128 * PAGE * Hkv * D, seed + 130 + c, 0, None)
+        call("genllm_fill_normal_bf16", inf.v_pool, 128 * PAGE * Hkv * D, seed + 140 + c, 0, None)
+        qq = torch.empty((S, Hq, D), dtype=torch.bfloat16, device="cuda")
+        paged.fill_normal_bf16(qq, seed + 150 + c)
+        qs.append(qq)
+    op = torch.empty((S, Hq, D), dtype=torch.bfloat16, device="cuda")
+    pinfos = [mp.get_layer(c) for c in range(copies)]
+
+    def pre(i):
+        inf = pinfos[i % copies]
+        paged.paged_prefill(qs[i % copies], op, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, 128, S, Hkv,
+                            1.0 / np.sqrt(D), q_layout="token")
+
+    p_us, _ = time_launches(torch, pre, 40)
+    mp.close()
+    flops = 4 * D * Hq * S * (S + 1) // 2
+    tfl = flops / (p_us * 1e-6) / 1e12
+    return {"decode": {"n_keys": n_keys, "avg_launch_us": round(d_us, 3),
+                       "median_us": round(1e3 * statistics.median(d_ms), 3), "bytes": d_bytes,
+                       "GB_s": round(d_gbs, 1), "frac_hbm": round(d_gbs / HBM_PEAK_GBS, 4)},
+            "prefill": {"S": S, "avg_launch_us": round(p_us, 3), "flops": flops, "TFLOPS": round(tfl, 1),
+                        "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}}
+
+
 def longctx_cfg5(np, torch, paged, synth, call, iters=10):
     Hq, Hkv, D, N, pool, layers = 32, 8, 128, 32761, 4096, 36
     seed = synth.config_seed(5)
@@ -389,8 +490,8 @@ def main():
     torch.cuda.set_device(0)
     common = (np, torch, paged, synth, call)
     if args.only and args.only != "headline":
-        fn = {"append": append_cfg2, "prefill": prefill_cfg4, "longctx": longctx_cfg5,
-              "linear": linear_qkv, "copy": copy_calibration}[args.only]
+        fn = {"append": append_cfg2, "prefill": prefill_cfg4, "flash": flash_cfg4, "qwen35": qwen35_d256,
+              "longctx": longctx_cfg5, "linear": linear_qkv, "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, **fn(*common)}), flush=True)
         return
 
@@ -415,6 +516,7 @@ def main():
     }
     if not args.skip_secondary and not args.only:
         result["secondary"] = {"append_config2": append_cfg2(*common), "prefill_config4": prefill_cfg4(*common),
+                               "flash_config4": flash_cfg4(*common), "qwen35_head_dim_256": qwen35_d256(*common),
                                "longctx_config5": longctx_cfg5(*common), "linear_qkv_4b": linear_qkv(*common)}
     if not args.skip_cpu and not args.only:
         result["cpu_baseline"] = cpu_baseline(mgr, np, paged, synth, args, seed)
