@@ -8,8 +8,10 @@
 // Work split: a task = 8 rows (heads) of one token and one kind (q, k or v
 // rows); row r of a task sits on lanes 8r..8r+7.  Tasks are numbered kind by
 // kind, and each wave takes TPW consecutive tasks of one kind, issuing the
-// loads of all of them before any arithmetic so that a wave keeps TPW * 2 KiB
-// of reads in flight.
+// loads of all of them before any arithmetic.  One task (2 KiB of reads) per
+// wave and many waves keep more bytes in flight across the GPU than fewer
+// waves with more tasks each: the loads of a wave's later tasks wait behind
+// its first ones.
 //
 // K/q lanes: lane j of a row holds elements 4j + 32t + {0,1,2,3}, t = 0..D/32-1
 // (one 8-byte load per t).  That puts the CPU rms_norm's 32 running sums
@@ -41,7 +43,7 @@ namespace genllm {
 
 namespace {
 
-constexpr int TPW = 4;  // tasks per wave
+constexpr int TPW = 1;  // tasks per wave (measured at config 2: 1 and 2 beat 4; 8 is 1.5x slower than 4)
 
 // TR = rope_dim / 64: chunk t < TR of a lane rotates with chunk t + TR (the
 // pair (i, i + rope_dim/2)); chunks from 2 TR on pass through.  TR = D/64 is
