@@ -46,6 +46,22 @@ def test_prefill_vs_oracle(orc, Hq, Hkv, S, N, causal):
     ctx.close()
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,S,N,causal", [
+    (8, 4, 128, 128, 5000, True),    # 79 key tiles: the page ids are reloaded past tile 64
+    (4, 2, 128, 70, 4500, False),
+    (8, 2, 256, 64, 4200, True),     # the D = 256 kernel over 132 key tiles
+])
+def test_prefill_long_context_vs_oracle(orc, Hq, Hkv, D, S, N, causal):
+    """A chunk of S queries after N - S cached tokens, past the first block of
+    page ids the kernel fetches at once."""
+    pool = (N + 15) // 16 + 7
+    ctx = Context(orc, Hkv, D, pool, N, 6000 + S + N + D, nan_tail=True)
+    q = synth.normal_bf16(6100 + S + D, (Hq, S, D))
+    got = run_prefill(ctx, q, causal)
+    assert_attn_close(got, ctx.oracle(q, causal), f"long prefill Hq{Hq} D{D} S{S} N{N} causal{causal}")
+    ctx.close()
+
+
 def torch_reference(ctx, q_bits, heads, causal=True):
     """float32 attention on the GPU for the given q heads; K/V gathered from
     the pools through the page table."""
