@@ -447,20 +447,26 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 // Qwen3.5's head_dim (Qwen35.hpp:14-16).  A token row is 512 B (32 chunks of
 // 16 B); both 256-byte halves carry the swizzle above (chunk c of row r at
 // position 16 (c / 16) + ((c % 16) ^ swz(r % 16))).  Two query blocks per wave
-// would need 128 accumulator registers here, so each wave owns one 16-query
-// block and every key of the tile; key tiles are 32 tokens (2 pages), double
-// buffered in 64 KB of LDS (two workgroups per CU).  Wave w moves the K
-// (w even) or V (w odd) rows of page w / 2 of each tile.
-constexpr int KT256 = 32;
+// would need 128 accumulator registers here, so a wave owns one 16-query block
+// and one half of every key tile.  Workgroup: 8 waves, query blocks 0..3 (64
+// queries) x key halves 0..1 of key tiles of 64 tokens (4 pages), one
+// workgroup per CU (two 64 KB tile buffers); the two halves of a query block
+// are merged through LDS at the end.  Wave w moves the K (w even) or V (w odd)
+// rows of page w / 2 of each tile; one tile is in flight while the other is
+// computed.  The grid runs from the query tile with the most keys down.
+constexpr int KT256 = 64;
 constexpr int QW256 = 16;
-constexpr int WAVES256 = 4;
-constexpr int QT256 = QW256 * WAVES256;
+constexpr int WAVES256 = 8;
+constexpr int QT256 = 4 * QW256;
 
 __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnParams p) {
     constexpr int D = 256;
     constexpr int KS = D / 32, DB = D / 16;
     constexpr int ROWB = D * 2;          // 512 bytes per token row
-    constexpr int TILEB = KT256 * ROWB;  // 16 KB of K (or V) per tile
+    constexpr int TILEB = KT256 * ROWB;  // 32 KB of K (or V) per tile
+    constexpr int KH = KT256 / 2;        // keys of a tile per wave
+    constexpr int XCH = DB * 4 + 2;      // floats per lane handed over at the end: O^T, m, l
+    static_assert(2 * XCH * 64 * 4 <= 2 * TILEB, "two hand-overs fit one buffer");
     __shared__ __attribute__((aligned(16))) char lds_b0[2 * TILEB];
     __shared__ __attribute__((aligned(16))) char lds_b1[2 * TILEB];
     lds_char* const buf0 = (lds_char*)lds_b0;
@@ -468,27 +474,25 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qblk = wv >> 1, kh = wv & 1;  // query block, key half
     const int n16 = lane & 15, g = lane >> 4;
     const int n_qt = (p.S + QT256 - 1) / QT256;
     const int rank = int(blockIdx.x) / p.Hq;
     const int hq = int(blockIdx.x) - rank * p.Hq;
-    const int heavy = (n_qt + 1) / 2;
-    const int qt = rank < heavy ? n_qt - 1 - rank : rank - heavy;  // heavy and light tiles paired
+    const int qt = n_qt - 1 - rank;
     const int hkv = hq / p.G;
     const int qabs0 = p.n_cached - p.S;
-    const int q0 = qt * QT256 + wv * QW256;
+    const int q0 = qt * QT256 + qblk * QW256;
+    const int n_cached = p.n_cached;
 
+    // Q^T operands: lane -> query q0 + n16, dims 32ks + 8g..+7 (a query past
+    // the chunk loads the last row: its column stays finite and is not written)
     bf16x8_t qb[KS];
     {
-        const int s = q0 + n16;
-        const bool ok = s < p.S;
-        const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(ok ? s : p.S - 1) * p.q_tok_stride;
+        const int s = min(q0 + n16, p.S - 1);
+        const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(s) * p.q_tok_stride;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            uint4 u = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
-            if (!ok) u = make_uint4(0, 0, 0, 0);
-            qb[ks] = as_bf16x8(u);
-        }
+        for (int ks = 0; ks < KS; ++ks) qb[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g));
     }
     float m = -INFINITY, l = 0.0f;
     f32x4_t acc[DB];
@@ -496,31 +500,29 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
     for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int wg_last = min(qt * QT256 + QT256, p.S) - 1;
-    const int kv_end = p.causal ? min(qabs0 + wg_last + 1, p.n_cached) : p.n_cached;
+    const int kv_end = p.causal ? min(qabs0 + wg_last + 1, n_cached) : n_cached;
     const int n_tiles = (kv_end + KT256 - 1) / KT256;
     const bool wave_has_rows = q0 < p.S;
-    const int w_last_abs = qabs0 + min(q0 + QW256, p.S) - 1;
-    const int wave_lim = p.causal ? min(qabs0 + q0 + 1, p.n_cached) : p.n_cached;
+    // keys below wave_lim are visible to every query of the wave, keys at or
+    // past wave_end to none of them
+    const int wave_lim = p.causal ? min(qabs0 + q0 + 1, n_cached) : n_cached;
+    const int wave_end = !wave_has_rows ? 0 : p.causal ? min(qabs0 + min(q0 + QW256, p.S), n_cached) : n_cached;
 
-    // ---- staging: wave w moves kind w % 2 (K, V) of page w / 2 of each tile;
-    // lanes 0..1 hold the tile's two K ids, lanes 2..3 the V ids
-    const int32_t* const k_ids = p.k_ids;
-    const int32_t* const v_ids = p.v_ids;
-    const bool paged = k_ids != nullptr;
-    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
+    // ---- staging: wave w moves kind w % 2 (K, V) of page w / 2 of each tile
+    const bool paged = p.k_ids != nullptr;
     const int kind = wv & 1, pg = wv >> 1;
+    const int32_t* const my_ids = kind ? p.v_ids : p.k_ids;
+    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
     const uint16_t* const src = (kind ? p.v_pool : p.k_pool) + head_off;
     const int64_t kv_row = p.kv_row, page_elems = p.page_elems;
-    const int n_cached = p.n_cached;
-    auto load_ids = [&](int tile) -> int {
-        const int page = 2 * tile + (lane & 1);
-        int id = 0;
-        if (lane < 4 && page * kPage < kv_end) id = !paged ? page : lane < 2 ? k_ids[page] : v_ids[page];
-        return id;
+    const int kv_row_bytes = int(kv_row) * 2;
+    // lane i <- the id of this wave's page of tile t0 + i
+    auto load_ids = [&](int t0) -> int {
+        const int page = 4 * (t0 + lane) + pg;
+        return page * kPage < kv_end ? my_ids[page] : 0;
     };
     // instruction e fills rows 2e, 2e+1 of the page: lane -> row 2e + lane/32,
     // position lane%32 <- chunk 16 (p/16) + ((p%16) ^ swz(row))
-    const int kv_row_bytes = int(kv_row) * 2;
     uint32_t dma_off[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -528,53 +530,41 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
         const int chunk = 16 * (pos >> 4) + ((pos & 15) ^ swz(row));
         dma_off[e] = uint32_t(row * kv_row_bytes + 16 * chunk);
     }
-    const uint32_t page_span = uint32_t(15 * kv_row_bytes + ROWB);
     const int dst0 = kind * TILEB + pg * (kPage * ROWB);
-    auto issue_tile = [&](int tile, int ids, lds_char* buf) {
-        const int tok_page = tile * KT256 + kPage * pg;
-        int64_t base;
-        uint32_t span;
-        if (paged) {
-            base = int64_t(__builtin_amdgcn_readlane(ids, 2 * kind + pg)) * page_elems;
-            span = page_span;
-        } else {
-            base = int64_t(tok_page) * kv_row;
-            span = uint32_t(__builtin_amdgcn_readfirstlane(max(min(n_cached - tok_page, kPage), 0) * kv_row_bytes));
-        }
+    // The buffer resource of a page spans exactly its rows below kv_end, so
+    // rows past the causal limit, the cache end or the table read as zeros:
+    // their keys are masked and their zero values meet zero probabilities.
+    auto issue_tile = [&](int t, int ids, lds_char* buf) {
+        const int tok_page = t * KT256 + kPage * pg;
+        const int valid = min(max(kv_end - tok_page, 0), kPage);
+        const uint32_t span = uint32_t(__builtin_amdgcn_readfirstlane(valid > 0 ? (valid - 1) * kv_row_bytes + ROWB : 0));
+        const int64_t base = paged ? int64_t(__builtin_amdgcn_readlane(ids, t & (IDS_BLOCK - 1))) * page_elems
+                                   : int64_t(tok_page) * kv_row;
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)(src + base), 0, span, kBufferFlags);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(buf + (dst0 + e * 1024)),
                                                      16, dma_off[e], 0, 0, 0);
     };
-    // V rows at or past kv_end are zeroed by the wave that loaded them
-    auto clear_tail = [&](int tile, lds_char* buf) {
-        if (kind == 0) return;
-        const int first = tile * KT256 + kPage * pg;
-        if (first + kPage <= kv_end) return;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int row = 2 * e + (lane >> 5);
-            if (first + row >= kv_end)
-                *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(buf + (dst0 + e * 1024 + 16 * lane)) =
-                    u32x4_t{0u, 0u, 0u, 0u};
-        }
-    };
 
+    // ---- this wave's 32 keys of one tile against its 16 queries (buf: K at
+    // 0, V at TILEB).  masked: the keys reach past the first query of the wave
+    // or past the cache end.
+    const float c = fmaxf(p.scale_log2, __FLT_MIN__);  // > 0: masked -inf scores give exactly 0
     auto compute_tile = [&](int t, const lds_char* buf, bool masked) {
-        const int tok0 = t * KT256;
+        const int tok0 = t * KT256 + KH * kh;  // first key of the half
+        const int r0 = KH * kh;                // its first LDS row (a multiple of 16)
         f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const int row = 16 * kb + n16;
+                const int row = r0 + 16 * kb + n16;
                 const int pos = 16 * (ks >> 2) + ((4 * (ks & 3) + g) ^ swz(n16));
                 const u32x4_t a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
                     buf + (row * ROWB + pos * 16));
                 s[kb] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[ks], s[kb]);
             }
-        const float c = fmaxf(p.scale_log2, __FLT_MIN__);  // > 0: masked -inf scores give exactly 0
         if (masked) {
             __asm__ volatile("");  // keep a branch: full tiles carry no selects
             const int qpos = qabs0 + q0 + n16;
@@ -603,26 +593,19 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
             for (int db = 0; db < DB; ++db) acc[db] *= alpha;
         }
         const float mu = m == -INFINITY ? 0.0f : m;
-        float sum = 0.0f;
+        float e[2][4];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float e = exp2_fast(__builtin_fmaf(s[kb][i], c, -mu));
-                s[kb][i] = e;
-                sum += e;
-            }
-        l += sum;
-        uint4 u;
-        u.x = bf16_pair_rne(s[0][0], s[0][1]);
-        u.y = bf16_pair_rne(s[0][2], s[0][3]);
-        u.z = bf16_pair_rne(s[1][0], s[1][1]);
-        u.w = bf16_pair_rne(s[1][2], s[1][3]);
-        const bf16x8_t pb = as_bf16x8(u);
-        // V^T from two transposing reads per 16 dims: rows 4g + n16/4 and + 16,
-        // dims 16db + 4(n16%4)..+3 (chunk 2db + (n16%4)/2, half n16%2); one
-        // integer offset per read (see the D = 128 kernel)
-        const int row0 = 4 * g + (n16 >> 2), row1 = row0 + 16;
+            for (int i = 0; i < 4; ++i) e[kb][i] = exp2_fast(__builtin_fmaf(s[kb][i], c, -mu));
+        l += ((e[0][0] + e[0][1]) + (e[0][2] + e[0][3])) + ((e[1][0] + e[1][1]) + (e[1][2] + e[1][3]));
+        const bf16x8_t pb = __builtin_bit_cast(
+            bf16x8_t, u32x4_t{bf16_pair_rne(e[0][0], e[0][1]), bf16_pair_rne(e[0][2], e[0][3]),
+                              bf16_pair_rne(e[1][0], e[1][1]), bf16_pair_rne(e[1][2], e[1][3])});
+        // V^T from two transposing reads per 16 dims: rows r0 + 4g + n16/4 and
+        // + 16, dims 16db + 4(n16%4)..+3 (chunk 2db + (n16%4)/2, half n16%2);
+        // one integer offset per read (see the D = 128 kernel)
+        const int row0 = r0 + 4 * g + (n16 >> 2), row1 = row0 + 16;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const int chunk = 2 * db + ((n16 & 3) >> 1), half = (n16 & 1) * 8;
@@ -636,31 +619,53 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
         }
     };
 
-    int ids_next = 0;
-    if (n_tiles > 0) {
-        const int ids0 = load_ids(0);
-        if (n_tiles > 1) ids_next = load_ids(1);
+    // ---- pipeline: one barrier per tile, two buffers.  Step t waits for its
+    // own loads of tile t, meets the other waves (tile t complete in LDS;
+    // everybody done with tile t-1), starts tile t+1 into the other buffer,
+    // then computes its half of tile t.  Every step issues the same 8 loads
+    // per wave; a tile past the last one has no rows below kv_end and reads
+    // as zeros.  Page ids arrive IDS_BLOCK tiles per load; the rare reload
+    // drains the loads in flight.
+    int ids = paged ? load_ids(0) : 0;
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // q and ids landed
+    issue_tile(0, ids, buf0);
+    auto step = [&](int t, const lds_char* cur, lds_char* nxt) {
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        issue_tile(0, ids0, buf0);
-    }
-    auto step = [&](int t, lds_char* cur, lds_char* nxt) {
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        clear_tail(t, cur);
-        __syncthreads();
-        if (t + 1 < n_tiles) {
-            issue_tile(t + 1, ids_next, nxt);
-            if (t + 2 < n_tiles) ids_next = load_ids(t + 2);
+        tile_barrier();
+        if (((t + 1) & (IDS_BLOCK - 1)) == 0 && t + 1 < n_tiles) {
+            if (paged) ids = load_ids(t + 1);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         }
-        const int tok0 = t * KT256;
-        if (wave_has_rows && !(p.causal && tok0 > w_last_abs)) compute_tile(t, cur, tok0 + KT256 > wave_lim);
+        issue_tile(t + 1, ids, nxt);
+        const int tok0 = t * KT256 + KH * kh;
+        if (tok0 < wave_end) compute_tile(t, cur, tok0 + KH > wave_lim);
     };
     for (int t = 0; t < n_tiles; t += 2) {
         step(t, buf0, buf1);
-        if (t + 1 < n_tiles) step(t + 1, buf1, buf0);
+        step(t + 1, buf1, buf0);
     }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the trailing (empty) loads have landed: LDS is free
 
-    if (!wave_has_rows) return;
-    float lt = l;
+    // ---- merge the two key halves of each query block: the key-half-1 wave
+    // stores (O^T, m, l) as [value][lane] floats, the key-half-0 wave combines
+    // m = max(m0, m1), O = O0 2^(m0-m) + O1 2^(m1-m), l likewise (a half that
+    // saw no key has m = -inf, weight 0) and writes the output.
+    __syncthreads();  // every wave is done with the tiles
+    lds_float* const xch = (lds_float*)((qblk >> 1) == 0 ? buf0 : buf1) + (qblk & 1) * XCH * 64 + lane;
+    if (kh == 1) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xch[(db * 4 + i) * 64] = acc[db][i];
+        xch[(DB * 4) * 64] = m;
+        xch[(DB * 4 + 1) * 64] = l;
+    }
+    __syncthreads();
+    if (kh == 1 || !wave_has_rows) return;
+    const float m1 = xch[(DB * 4) * 64], l1 = xch[(DB * 4 + 1) * 64];
+    const float mt = fmaxf(m, m1);
+    const float a0 = mt == -INFINITY ? 0.0f : exp2_fast(m - mt), a1 = mt == -INFINITY ? 0.0f : exp2_fast(m1 - mt);
+    float lt = l * a0 + l1 * a1;
     lt += __shfl_xor(lt, 16);
     lt += __shfl_xor(lt, 32);
     const float inv = 1.0f / lt;
@@ -669,9 +674,12 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
     uint16_t* orow = p.out + int64_t(hq) * p.o_head_stride + int64_t(s) * p.o_tok_stride;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (acc[db][i] * a0 + xch[(db * 4 + i) * 64] * a1) * inv;
         uint2 w;
-        w.x = bf16_pair_out(acc[db][0] * inv, acc[db][1] * inv);
-        w.y = bf16_pair_out(acc[db][2] * inv, acc[db][3] * inv);
+        w.x = bf16_pair_out(o[0], o[1]);
+        w.y = bf16_pair_out(o[2], o[3]);
         *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = w;
     }
 }
