@@ -19,10 +19,13 @@
 // (A product of two bf16 values is exact in fp32, so the fused and unfused
 // forms of the 8-element group agree.)
 //
-// More rows: rocBLAS gemm_ex (bf16 inputs, fp32 compute, fp32 result in the
-// caller's workspace), then linear_epilogue_kernel adds the bias in fp32 and
-// rounds once; the summation order is rocBLAS's, so results match the
-// reference within fp32 accumulation error, not bit for bit.
+// More rows: rocBLAS gemm_ex, bf16 inputs and fp32 compute.  With a bias, the
+// fp32 result goes to the caller's workspace and linear_epilogue_kernel adds
+// the bias in fp32 and rounds once; without one (Qwen3's projections), rocBLAS
+// writes bf16 directly, rounding the fp32 result once to nearest even (an
+// fp32 subnormal result stays a bf16 subnormal where the reference flushes it
+// to zero).  The summation order is rocBLAS's, so results match the reference
+// within fp32 accumulation error, not bit for bit.
 #include <rocblas/rocblas.h>
 
 #include <map>
@@ -224,7 +227,7 @@ int launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, ui
         return GENLLM_OK;
     }
     const size_t need = linear_workspace_bytes(rows, common, cols);
-    if (!workspace || workspace_bytes < need)
+    if (bias && (!workspace || workspace_bytes < need))
         return fail(GENLLM_ERR_INVALID, "linear: workspace too small (need " + std::to_string(need) + " bytes, have " +
                                             std::to_string(workspace_bytes) + ")");
     rocblas_handle hb = nullptr;
@@ -232,6 +235,17 @@ int launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, ui
     if (rocblas_set_stream(hb, stream) != rocblas_status_success)
         return fail(GENLLM_ERR_HIP, "linear: rocblas_set_stream failed");
     const float alpha = 1.0f, beta = 0.0f;
+    if (!bias) {
+        // column-major view: out^T [cols][rows] = (w as [common][cols])^T * (x as [common][rows])
+        const rocblas_status st = rocblas_gemm_ex(
+            hb, rocblas_operation_transpose, rocblas_operation_none, rocblas_int(cols), rocblas_int(rows),
+            rocblas_int(common), &alpha, w, rocblas_datatype_bf16_r, rocblas_int(common), x, rocblas_datatype_bf16_r,
+            rocblas_int(common), &beta, out, rocblas_datatype_bf16_r, rocblas_int(cols), out, rocblas_datatype_bf16_r,
+            rocblas_int(cols), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success)
+            return fail(GENLLM_ERR_HIP, std::string("linear: rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+        return GENLLM_OK;
+    }
     float* acc = static_cast<float*>(workspace);
     // column-major view: acc^T [cols][rows] = (w as [common][cols])^T * (x as [common][rows])
     const rocblas_status st = rocblas_gemm_ex(

@@ -211,9 +211,12 @@ int genllm_flash_attention(const void *q, const void *k, const void *v, void *ou
  * out [rows][cols], all bf16 on the device; fp32 accumulation, the bias added
  * in fp32, one rounding.  rows <= 4 with common % 8 == 0: the reference CPU
  * summation order exactly (bit-identical results) and no workspace.  Other
- * shapes: rocBLAS GEMM into an fp32 workspace of
- * genllm_linear_workspace_bytes(rows, common, cols) bytes (0 when none is
- * needed); GENLLM_ERR_INVALID if it is missing or smaller. */
+ * shapes: rocBLAS GEMM (fp32 accumulation in rocBLAS's order).  With a bias
+ * it writes into an fp32 workspace of genllm_linear_workspace_bytes(rows,
+ * common, cols) bytes (0 when none is needed; GENLLM_ERR_INVALID if it is
+ * missing or smaller) and a second kernel adds the bias and rounds; without a
+ * bias it rounds straight into out (round to nearest even; an fp32 subnormal
+ * result stays a bf16 subnormal) and the workspace is not used. */
 size_t genllm_linear_workspace_bytes(int64_t rows, int64_t common, int64_t cols);
 int genllm_linear(const void *x, const void *w, const void *bias, void *out, int64_t rows, int64_t common,
                   int64_t cols, void *workspace, size_t workspace_bytes, void *stream);

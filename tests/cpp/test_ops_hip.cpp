@@ -412,7 +412,7 @@ bool run_linear(int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_
 }
 
 bool test_linear_decode() { return run_linear(1, 2560, 1024, false, 31, true) && run_linear(3, 1024, 300, true, 32, true); }
-bool test_linear_prefill() { return run_linear(64, 1024, 512, true, 33, false); }
+bool test_linear_prefill() { return run_linear(64, 1024, 512, true, 33, false) && run_linear(64, 1024, 512, false, 34, false); }
 
 }  // namespace
 

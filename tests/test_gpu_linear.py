@@ -70,20 +70,25 @@ def test_linear_gemv_order_cases(orc):
     assert np.array_equal(got, orc.linear(xb, wb))
 
 
-@pytest.mark.parametrize("rows,common,cols", [
-    (5, 2560, 512),
-    (64, 1024, 1024),
-    (300, 2560, 640),
-    (2, 20, 33),       # common % 8 != 0 also takes the GEMM path
+@pytest.mark.parametrize("rows,common,cols,with_bias", [
+    (5, 2560, 512, True),
+    (64, 1024, 1024, True),
+    (300, 2560, 640, True),
+    (2, 20, 33, True),       # common % 8 != 0 also takes the GEMM path
+    (64, 1024, 1024, False),  # no bias: rocBLAS rounds straight into out
+    (2048, 2560, 768, False),
 ])
-def test_linear_gemm_within_tolerance(orc, rows, common, cols):
+def test_linear_gemm_within_tolerance(orc, rows, common, cols, with_bias):
     x, w, b = inputs(rows + common + cols, rows, common, cols)
+    if not with_bias:
+        b = None
     assert paged.linear_workspace_bytes(rows, common, cols) == rows * cols * 4
     got = synth.bf16_bits_to_f32(run_linear(x, w, b)).astype(np.float64)
     want = orc.linear(x, w, b)
     xf, wf = synth.bf16_bits_to_f32(x).astype(np.float64), synth.bf16_bits_to_f32(w).astype(np.float64)
-    exact = xf @ wf.T + synth.bf16_bits_to_f32(b).astype(np.float64)[None, :]
-    mag = np.abs(xf) @ np.abs(wf).T + np.abs(synth.bf16_bits_to_f32(b))[None, :]
+    bf = synth.bf16_bits_to_f32(b).astype(np.float64) if b is not None else np.zeros(cols)
+    exact = xf @ wf.T + bf[None, :]
+    mag = np.abs(xf) @ np.abs(wf).T + np.abs(bf)[None, :]
     e = np.abs(exact)
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(e, 2.0 ** -126))) - 7)
     tol = ulp / 2 + common * 2.0 ** -24 * mag  # one bf16 rounding + fp32 accumulation
@@ -97,11 +102,13 @@ def test_linear_errors():
     x = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
     w = torch.zeros((16, 64), dtype=torch.bfloat16, device="cuda")
     out = torch.empty((8, 16), dtype=torch.bfloat16, device="cuda")
+    bias = torch.zeros((16,), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(GenllmError):
-        paged.linear(x, w, out)  # 8 rows need a workspace
+        paged.linear(x, w, out, bias=bias)  # 8 rows with a bias need a workspace
     small = torch.empty(8 * 16 * 4 - 4, dtype=torch.uint8, device="cuda")
     with pytest.raises(GenllmError):
-        paged.linear(x, w, out, workspace=small)
+        paged.linear(x, w, out, bias=bias, workspace=small)
+    paged.linear(x, w, out)  # without a bias the GEMM rounds straight into out: no workspace
     with pytest.raises(GenllmError):
         call("genllm_linear", None, w.data_ptr(), None, out.data_ptr(), 1, 64, 16, None, 0, None)
     # zero rows: nothing to do
