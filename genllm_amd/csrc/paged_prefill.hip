@@ -147,6 +147,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     // that a masked score of -inf gives exp2(-inf * c - m) = 0 without a
     // select; at scale 0 every weight stays exp2(~0) = 1.
     const float c = fmaxf(p.scale_log2, __FLT_MIN__);
+    const float inv_c = 1.0f / c;  // may be inf (then no row grows after its first tile)
 
     // ---- tile staging.  Wave (qg, kq) moves page kq of every tile: its K
     // rows (qg 0) or its V rows (qg 1).
@@ -193,6 +194,9 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
         // softmax state of query 16b + n16 (per lane, equal over the lane's
         // 16-lane row group for m), O^T columns of query 16 hb + n16
         float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+        // kept beside m: nm = -m (0 while m = -inf), and th = the raw score
+        // above which the scaled score exceeds m + 8 (-inf while m = -inf)
+        float nm[2] = {0.0f, 0.0f}, th[2] = {-INFINITY, -INFINITY};
         f32x16_t acc[DJ];
 #pragma unroll
         for (int j = 0; j < DJ; ++j)
@@ -265,23 +269,27 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
             }
             // Online softmax with a lazy rescale: a row's reference max only
             // moves (and its l, O^T are rescaled) when the tile max exceeds it
-            // by more than 2^8, so p <= 256; a lane's own keys decide whether
-            // any row may grow, and the row max (two cross-lane steps) is
-            // formed only then.
+            // by about 2^8 (its raw max passes th), so p <= 256 or so; a
+            // lane's own keys decide whether any row may grow, and the row max
+            // (two cross-lane steps) is formed only then.
             float mx[2];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) mx[b] = fmaxf(fmaxf(s[b][0], s[b][1]), fmaxf(s[b][2], s[b][3])) * c;
-            if (__any(mx[0] > m[0] + 8.0f || mx[1] > m[1] + 8.0f)) {
+            for (int b = 0; b < 2; ++b)  // IEEE maximum (NaN-propagating): v_maximum3_f32, no quieting
+                mx[b] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s[b][0], s[b][1]),
+                                                      __builtin_elementwise_maximum(s[b][2], s[b][3]));
+            if (__any(mx[0] > th[0] || mx[1] > th[1])) {
                 float alpha[2];
 #pragma unroll
                 for (int b = 0; b < 2; ++b) {
                     float r = fmaxf(mx[b], __shfl_xor(mx[b], 16));
                     r = fmaxf(r, __shfl_xor(r, 32));
-                    const bool grow = r > m[b] + 8.0f;
-                    const float mn = grow ? r : m[b];
+                    const bool grow = r > th[b];
+                    const float mn = grow ? r * c : m[b];
                     alpha[b] = grow ? exp2_fast(m[b] - mn) : 1.0f;
                     l[b] *= alpha[b];
                     m[b] = mn;
+                    nm[b] = grow ? -mn : nm[b];
+                    th[b] = grow ? (mn + 8.0f) * inv_c : th[b];
                 }
                 const float as = hb ? alpha[1] : alpha[0];
 #pragma unroll
@@ -290,10 +298,9 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
             uint32_t pk[2][2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const float mu = m[b] == -INFINITY ? 0.0f : m[b];
                 float e[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) e[i] = exp2_fast(__builtin_fmaf(s[b][i], c, -mu));  // masked: exactly 0
+                for (int i = 0; i < 4; ++i) e[i] = exp2_fast(__builtin_fmaf(s[b][i], c, nm[b]));  // masked: exactly 0
                 l[b] += (e[0] + e[1]) + (e[2] + e[3]);
                 pk[b][0] = bf16_pair_rne(e[0], e[1]);
                 pk[b][1] = bf16_pair_rne(e[2], e[3]);
@@ -495,6 +502,9 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
         for (int ks = 0; ks < KS; ++ks) qb[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g));
     }
     float m = -INFINITY, l = 0.0f;
+    // nm = -m (0 while m = -inf); th = the raw score above which the scaled
+    // score exceeds m + 8 (-inf while m = -inf)
+    float nm = 0.0f, th = -INFINITY;
     f32x4_t acc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -551,6 +561,7 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
     // 0, V at TILEB).  masked: the keys reach past the first query of the wave
     // or past the cache end.
     const float c = fmaxf(p.scale_log2, __FLT_MIN__);  // > 0: masked -inf scores give exactly 0
+    const float inv_c = 1.0f / c;                       // may be inf (then no row grows after its first tile)
     auto compute_tile = [&](int t, const lds_char* buf, bool masked) {
         const int tok0 = t * KT256 + KH * kh;  // first key of the half
         const int r0 = KH * kh;                // its first LDS row (a multiple of 16)
@@ -575,29 +586,29 @@ __global__ __launch_bounds__(WAVES256 * 64) void paged_prefill_d256_kernel(AttnP
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[kb][i] = (16 * kb + i < rel) ? s[kb][i] : -INFINITY;
         }
-        float mr = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mr = fmaxf(mr, s[kb][i]);
-        float mx = mr * c;
-        if (__any(mx > m + 8.0f)) {  // lazy rescale, as in the D = 128 kernel
+        // raw row max, IEEE maximum (NaN-propagating: v_maximum3_f32, no quieting)
+        float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s[0][0], s[0][1]),
+                                                 __builtin_elementwise_maximum(s[0][2], s[0][3]));
+        mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(__builtin_elementwise_maximum(s[1][0], s[1][1]),
+                                                                             __builtin_elementwise_maximum(s[1][2], s[1][3])));
+        if (__any(mx > th)) {  // lazy rescale, as in the D = 128 kernel
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const bool grow = mx > m + 8.0f;
-            const float mn = grow ? mx : m;
+            const bool grow = mx > th;
+            const float mn = grow ? mx * c : m;
             const float alpha = grow ? exp2_fast(m - mn) : 1.0f;
             l *= alpha;
             m = mn;
+            nm = grow ? -mn : nm;
+            th = grow ? (mn + 8.0f) * inv_c : th;
 #pragma unroll
             for (int db = 0; db < DB; ++db) acc[db] *= alpha;
         }
-        const float mu = m == -INFINITY ? 0.0f : m;
         float e[2][4];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) e[kb][i] = exp2_fast(__builtin_fmaf(s[kb][i], c, -mu));
+            for (int i = 0; i < 4; ++i) e[kb][i] = exp2_fast(__builtin_fmaf(s[kb][i], c, nm));
         l += ((e[0][0] + e[0][1]) + (e[0][2] + e[0][3])) + ((e[1][0] + e[1][1]) + (e[1][2] + e[1][3]));
         const bf16x8_t pb = __builtin_bit_cast(
             bf16x8_t, u32x4_t{bf16_pair_rne(e[0][0], e[0][1]), bf16_pair_rne(e[0][2], e[0][3]),
