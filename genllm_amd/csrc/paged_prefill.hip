@@ -15,10 +15,13 @@
 // queries of group qg, and the four partial softmax states of a group are
 // merged through LDS at the end.
 // Key tiles are staged in four LDS buffers (three tiles in flight), K and V
-// each as [token][dim] rows of 256 B whose 16-byte chunks are XOR-swizzled
-// (chunk c of row r at position c ^ swz(r % 16), swz(r) = 2 (r % 8) + r / 8),
-// which keeps both the K operand reads and the transposing V reads free of LDS
-// bank conflicts.  Wave (qg, kq) moves the K (qg 0) or V (qg 1) rows of page
+// each as [token][dim] rows of 256 B whose 16-byte chunks are swizzled: chunk c
+// of row r sits at position cperm(c) ^ swz(r % 16), with swz(r) = 2 (r % 8) +
+// r / 8 and cperm swapping bits 1 and 3 of c.  The K operand reads (16 rows,
+// one chunk each) cover 16 distinct positions; in a transposing V read the
+// two 16-lane halves of a 32-lane group (dims 0-15 and 16-31 of a 32-dim
+// block, chunk bit 1) land in different 128-byte halves of the rows (position
+// bit 3), so the row XOR no longer folds them onto the same banks.  Wave (qg, kq) moves the K (qg 0) or V (qg 1) rows of page
 // kq of every tile straight from HBM into LDS with 16-byte buffer loads in LDS
 // mode (lane i's 16 bytes land at base + 16 i), so a tile costs no registers,
 // no VALU and no LDS store instructions; one buffer resource per page (base =
@@ -68,6 +71,8 @@ __device__ __forceinline__ uint32_t bf16_pair_rne(float lo, float hi) {
 // chunk-position swizzle of a 256-byte LDS row: bijective on r % 16, and
 // 2 (r % 8) separates the 32-byte chunk pairs of eight consecutive rows
 __device__ __forceinline__ constexpr int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// chunk-index bit swap (1 <-> 3) applied before the row XOR (an involution)
+__device__ __forceinline__ constexpr int cperm(int c) { return (c & 5) | ((c & 2) << 2) | ((c & 8) >> 2); }
 
 __device__ __forceinline__ s16x4_t ds_read_tr(const lds_char* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -160,12 +165,12 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
     // Lane byte offsets inside a page, the same for every tile: instruction e
     // fills rows 4e..4e+3, lane -> row 4e + lane/16 (rows start on page
     // boundaries, so row % 16 is that slot), position lane%16 <- chunk
-    // (lane%16) ^ swz(slot).
+    // cperm((lane%16) ^ swz(slot)).
     uint32_t dma_off[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int slot = 4 * e + (lane >> 4);
-        dma_off[e] = uint32_t(slot * kv_row_bytes + 16 * ((lane & 15) ^ swz(slot)));
+        dma_off[e] = uint32_t(slot * kv_row_bytes + 16 * cperm((lane & 15) ^ swz(slot)));
     }
     const int dst_wave = qg * TILEB + kq * PAGEB;
 
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const u32x4_t a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
-                    buf + (krow * ROWB + (((4 * ks + g) ^ swz(n16)) * 16)));
+                    buf + (krow * ROWB + ((cperm(4 * ks + g) ^ swz(n16)) * 16)));
 #pragma unroll
                 for (int b = 0; b < 2; ++b) s[b] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[b][ks], s[b]);
             }
@@ -327,8 +332,8 @@ __global__ __launch_bounds__(WAVES * 64) void paged_prefill_kernel(AttnParams p)
 #pragma unroll
             for (int j = 0; j < DJ; ++j) {
                 const int chunk = 4 * j + 2 * hb + ((n16 & 3) >> 1), half = (n16 & 1) * 8;
-                const s16x4_t lo = ds_read_tr(buf + (TILEB + vrow0 * ROWB + ((chunk ^ vsw0) * 16) + half));
-                const s16x4_t hi = ds_read_tr(buf + (TILEB + vrow1 * ROWB + ((chunk ^ vsw1) * 16) + half));
+                const s16x4_t lo = ds_read_tr(buf + (TILEB + vrow0 * ROWB + ((cperm(chunk) ^ vsw0) * 16) + half));
+                const s16x4_t hi = ds_read_tr(buf + (TILEB + vrow1 * ROWB + ((cperm(chunk) ^ vsw1) * 16) + half));
                 const s16x4_t a8[2] = {lo, hi};
                 acc[j] = mfma32x32x16(__builtin_bit_cast(bf16x8_t, a8), pb, acc[j]);
             }
