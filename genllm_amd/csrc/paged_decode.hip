@@ -46,7 +46,7 @@ namespace genllm {
 namespace {
 constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
 constexpr int kWaves = 4;       // waves of a split workgroup
-constexpr int kMergeWaves = 4;  // waves of a merge workgroup
+constexpr int kMergeU = 16;     // splits in flight per merge lane
 constexpr int kMaxSplits = 256;
 // pages in flight per wave: 3 at D = 128 (two waves per SIMD fit), 2 at
 // D = 256 (a page then takes twice the registers)
@@ -355,15 +355,19 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
     }
 }
 
-// Merge of the splits: one workgroup per (row, kv head).  Wave w reduces the
-// splits w, w+4, ... to its own log-sum-exp partial (M_w, L_w, O_w): each lane
-// loads the o of its 2 dims and, as a broadcast, the (m, l) of each of those
-// splits, up to 16 splits before any arithmetic (one memory round trip for up
-// to 64 splits); the 4 partials then meet in LDS with the same rule
+// Merge of the splits: one workgroup of MW waves per (row, kv head).  Wave w
+// reduces the splits w, w+MW, ... to its own log-sum-exp partial (M_w, L_w,
+// O_w): each lane loads the o of its dims and, as a broadcast, the (m, l) of
+// each of those splits, up to kMergeU splits before any arithmetic (one memory
+// round trip for up to MW * kMergeU splits); the MW partials then meet in LDS
+// with the same rule
 //   M = max M_w, L = sum L_w 2^(M_w - M), O = sum O_w 2^(M_w - M), out = O / L.
-template <int D>
-__global__ __launch_bounds__(kMergeWaves * 64) void paged_decode_merge_kernel(AttnParams p) {
-    constexpr int U = 16;        // splits in flight per lane
+// MW is 4, or 8 above 4 * kMergeU splits (measured: 8 waves cost about 0.4 us
+// at 31-32 splits and save 0.6 us at 103).
+template <int D, int MW>
+__global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams p) {
+    constexpr int kMergeWaves = MW;
+    constexpr int U = kMergeU;   // splits in flight per lane
     constexpr int VH = D / 128;  // lane -> dims 128 hh + 2 lane, +1
     __shared__ float s_o[kMergeWaves][D];
     __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
@@ -492,7 +496,10 @@ int launch_decode_d(const AttnParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(paged_decode_kernel<D>, dim3(p.n_splits, p.Hkv), dim3(kWaves * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1) {
-        hipLaunchKernelGGL(paged_decode_merge_kernel<D>, dim3(p.G * p.S, p.Hkv), dim3(kMergeWaves * 64), 0, stream, p);
+        if (p.n_splits > 4 * kMergeU)
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), dim3(p.G * p.S, p.Hkv), dim3(8 * 64), 0, stream, p);
+        else
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4>), dim3(p.G * p.S, p.Hkv), dim3(4 * 64), 0, stream, p);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;

@@ -132,6 +132,18 @@ def test_decode_repeat_is_deterministic(orc):
     ctx.close()
 
 
+@pytest.mark.parametrize("N,pps", [(1024, 1), (1025, 1), (2049, 1), (2049, 2), (4097, 1)])
+def test_decode_merge_workgroup_sizes(orc, N, pps):
+    """Split counts on both sides of the merge's 4-wave / 8-wave switch (64
+    splits): 64, 65, 129, 65 and 129 (257 pages exceed the 256-split cap, so
+    the plan raises pps to 2)."""
+    ctx = Context(orc, 8, 128, (N + 15) // 16 + 3, N, 500 + N, nan_tail=True)
+    q = synth.normal_bf16(600 + N, (32, 1, 128))
+    got, _ = ctx.decode(q, pps=pps)
+    assert_attn_close(got, ctx.oracle(q), f"N{N} pps{pps}")
+    ctx.close()
+
+
 @pytest.mark.parametrize("N,pps", [(1, None), (17, None), (300, None), (4099, None), (1000, 3)])
 def test_decode_qwen35_head_dim_256(orc, N, pps):
     """Qwen3.5 attention layer shape (Qwen35.hpp:14-16): 8 q heads, 2 kv heads,
