@@ -5,9 +5,14 @@
 //   out[q] = sum_t softmax_t(scale * q.k_t) v_t over keys t <= q_abs (causal)
 // with kv head h = q head / groups (:158) and q_abs = n_cached - S + s (:164).
 //
-// Split kernel: grid (splits, Hkv), 256 threads = 4 waves.  A workgroup owns
-// one kv head and a contiguous range of pages; its waves take pages
-// round-robin.  The rows of the kv head -- its (query, GQA q-head) pairs, at
+// Split kernel: grid (Hkv, splits), W = 4 or 8 waves.  A workgroup owns one
+// kv head and a contiguous range of pages; its waves take pages round-robin.
+// The kv head is the fastest grid index: the dispatcher deals workgroups to the
+// 8 XCDs round-robin, so with 8 kv heads every split of head h (and, with the
+// same order in the merge grid, that head's merge) runs on XCD h.  8 waves
+// serve short page ranges (at most kWideMaxPps pages, D = 128): each wave then
+// owns at most 4 pages, so a split finishes in fewer dependent memory round
+// trips.  Long ranges keep 4 waves, which holds fewer bytes in flight per CU.  The rows of the kv head -- its (query, GQA q-head) pairs, at
 // most 16 -- are the 16 columns of the MFMA tiles, so K/V are read once for all
 // of them.
 //
@@ -45,13 +50,16 @@ namespace genllm {
 
 namespace {
 constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
-constexpr int kWaves = 4;       // waves of a split workgroup
+constexpr int kWaves = 4;       // waves of a split workgroup (long page ranges)
+constexpr int kWideWaves = 8;   // waves of a split workgroup over short ranges (D = 128)
+constexpr int kWideMaxPps = 32; // pages per split up to which the 8-wave form runs
 constexpr int kMergeU = 16;     // splits in flight per merge lane
 constexpr int kMaxSplits = 256;
-// pages in flight per wave: 3 at D = 128 (two waves per SIMD fit), 2 at
-// D = 256 (a page then takes twice the registers)
+// pages in flight per wave: 1 at D = 128 (a wave requests page j+1 only after
+// page j's data has arrived; measured faster than 2 or 3 at 8K and 32K keys:
+// more bytes in flight per CU only lengthen the memory queues), 2 at D = 256
 template <int D>
-constexpr int kPagesInFlight = D == 128 ? 3 : 2;
+constexpr int kPagesInFlight = D == 128 ? 1 : 2;
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
 
 __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
@@ -65,21 +73,21 @@ struct PageRegs {
     uint4 v[4][D / 128];   // V rows of tokens 4g..4g+3, dims 8 n16 + 128 hh
 };
 
-template <int D>
-__global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p) {
+template <int D, int W>
+__global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     static_assert(D == 128 || D == 256, "decode kernel: head_dim 128 or 256");
     constexpr int KS = D / 32;   // S^T k-steps
     constexpr int DB = D / 16;   // O^T dim blocks
     constexpr int VH = D / 128;  // 128-dim halves of a V row per lane
     constexpr int PF = kPagesInFlight<D>;
 
-    __shared__ __attribute__((aligned(16))) uint16_t lds_vt[kWaves][D * VT_ROW];
-    __shared__ float lds_m[kWaves][kRows], lds_l[kWaves][kRows];
-    __shared__ float lds_o[kWaves][kRows][D + 4];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_vt[W][D * VT_ROW];
+    __shared__ float lds_m[W][kRows], lds_l[W][kRows];
+    __shared__ float lds_o[W][kRows][D + 4];
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n16 = lane & 15, g = lane >> 4;
-    const int sp = blockIdx.x, h = blockIdx.y;
+    const int h = blockIdx.x, sp = blockIdx.y;
     const int rows_total = p.G * p.S;  // <= 16
 
     // this lane's row (MFMA column): q head h*G + r%G, query r/G
@@ -99,7 +107,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
 
     const int begin = sp * p.pages_per_split;
     const int end = min(begin + p.pages_per_split, p.n_pages);
-    const int np = end - begin - wv > 0 ? (end - begin - wv + kWaves - 1) / kWaves : 0;
+    const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;
     // fused append: page ids opened by this call come from the launch arguments
     if (sp == 0 && h == 0 && threadIdx.x < p.upd.count) {
         p.k_ids_w[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
@@ -107,7 +115,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
     }
     int my_kid = 0, my_vid = 0;  // block-table entries of the wave's pages, one per lane
     if (lane < np) {
-        const int pg = begin + wv + kWaves * lane;
+        const int pg = begin + wv + W * lane;
         const int rel = pg - p.upd.first;
         if (rel >= 0 && rel < p.upd.count) {
             my_kid = p.upd.k[rel];
@@ -131,7 +139,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
     // tokens.  Only they take the per-token conditions below.
     const int lo_tok = min(p.causal ? p.n_cached - p.S + 1 : p.n_cached, p.new_from);
     const int special_from = lo_tok / kPage;
-    auto page_of = [&](int j) { return begin + wv + kWaves * j; };
+    auto page_of = [&](int j) { return begin + wv + W * j; };
 
     // Token t >= new_from is this call's append: read it from k_new / v_new.
     auto load_page = [&](int j, PageRegs<D>& pr, bool special) {
@@ -315,16 +323,16 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
 
     // workgroup merge: wave -> rows ri, ri+4, ...; lane -> dims d2, d2+1 of
     // each 128-dim half
-    for (int ri = wv; ri < rows_total; ri += kWaves) {
+    for (int ri = wv; ri < rows_total; ri += W) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, lds_m[w2][ri]);
+        for (int w2 = 0; w2 < W; ++w2) M = fmaxf(M, lds_m[w2][ri]);
         float L = 0.0f, O0[VH], O1[VH];
 #pragma unroll
         for (int hh = 0; hh < VH; ++hh) O0[hh] = O1[hh] = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int w2 = 0; w2 < kWaves; ++w2) {
+            for (int w2 = 0; w2 < W; ++w2) {
                 const float e = exp2_fast(lds_m[w2][ri] - M);
                 L += lds_l[w2][ri] * e;
 #pragma unroll
@@ -355,7 +363,8 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(AttnParams p)
     }
 }
 
-// Merge of the splits: one workgroup of MW waves per (row, kv head).  Wave w
+// Merge of the splits: one workgroup of MW waves per (kv head, row), grid
+// (Hkv, rows) in the split grid's XCD order.  Wave w
 // reduces the splits w, w+MW, ... to its own log-sum-exp partial (M_w, L_w,
 // O_w): each lane loads the o of its dims and, as a broadcast, the (m, l) of
 // each of those splits, up to kMergeU splits before any arithmetic (one memory
@@ -372,7 +381,7 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
     __shared__ float s_o[kMergeWaves][D];
     __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int ri = blockIdx.x, h = blockIdx.y;
+    const int h = blockIdx.x, ri = blockIdx.y;
     const int rows = p.G * p.S;
     const int ns = p.n_splits;  // <= kMaxSplits
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
@@ -493,13 +502,21 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
 
 template <int D>
 int launch_decode_d(const AttnParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL(paged_decode_kernel<D>, dim3(p.n_splits, p.Hkv), dim3(kWaves * 64), 0, stream, p);
+    bool wide = false;
+    if constexpr (D == 128) {
+        wide = p.pages_per_split <= kWideMaxPps;
+        if (wide)
+            hipLaunchKernelGGL((paged_decode_kernel<D, kWideWaves>), dim3(p.Hkv, p.n_splits), dim3(kWideWaves * 64), 0,
+                               stream, p);
+    }
+    if (!wide)
+        hipLaunchKernelGGL((paged_decode_kernel<D, kWaves>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1) {
         if (p.n_splits > 4 * kMergeU)
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), dim3(p.G * p.S, p.Hkv), dim3(8 * 64), 0, stream, p);
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), dim3(p.Hkv, p.G * p.S), dim3(8 * 64), 0, stream, p);
         else
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4>), dim3(p.G * p.S, p.Hkv), dim3(4 * 64), 0, stream, p);
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4>), dim3(p.Hkv, p.G * p.S), dim3(4 * 64), 0, stream, p);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;

@@ -110,6 +110,21 @@ def test_decode_split_plans(orc, pps):
     ctx.close()
 
 
+@pytest.mark.parametrize("pps", [17, 32, 33, 64])
+def test_decode_wave_forms(orc, pps):
+    """Head_dim 128 splits of at most 32 pages run 8-wave workgroups, longer
+    ones 4 waves; both forms against the oracle over 4100 keys (257 pages,
+    the last one partial), with a fresh and a stale workspace."""
+    ctx = Context(orc, 8, 128, 300, 4100, 91 + pps, nan_tail=True)
+    q = synth.normal_bf16(92 + pps, (32, 1, 128))
+    ref = ctx.oracle(q)
+    got, _ = ctx.decode(q, pps=pps)
+    assert_attn_close(got, ref, f"pps{pps}")
+    got2, _ = ctx.decode(q, pps=pps)
+    assert np.array_equal(got, got2)
+    ctx.close()
+
+
 @pytest.mark.parametrize("S,Hq,causal", [(2, 32, True), (4, 32, True), (3, 16, True), (8, 16, True),
                                          (2, 32, False)])
 def test_decode_multi_query(orc, S, Hq, causal):
