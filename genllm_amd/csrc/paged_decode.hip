@@ -61,6 +61,7 @@ constexpr int kMaxSplits = 256;
 template <int D>
 constexpr int kPagesInFlight = D == 128 ? 1 : 2;
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
+constexpr int kNonTemporal = 2;    // buffer-load cache policy bit nt (gfx950: sc0 = 1, nt = 2, sc1 = 16)
 
 __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
     const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
@@ -149,18 +150,21 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         if (!special) {
             // buffer loads: scalar page base in the resource (whose size bounds
             // every lane offset), 32-bit lane offset, row offset as immediate
-            // (K) or scalar offset (V)
+            // (K) or scalar offset (V); cache policy nt (2): every byte is read
+            // once per step, so the pages stream past L2 instead of evicting
+            // the page ids and partials (measured 13.33 -> 12.87 us at 8K keys,
+            // 30.2 -> 29.8 us per layer at 32K)
             const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kb), 0, page_bytes, kBufferFlags);
             const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb), 0, page_bytes, kBufferFlags);
 #pragma unroll
             for (int c = 0; c < KS; ++c)
-                pr.k[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, kcol_b + 64 * c, 0, 0));
+                pr.k[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, kcol_b + 64 * c, 0, kNonTemporal));
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int hh = 0; hh < VH; ++hh)
                     pr.v[i][hh] = __builtin_bit_cast(
-                        uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vcol_b + 256 * hh, i * kv_row_b, 0));
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vcol_b + 256 * hh, i * kv_row_b, kNonTemporal));
             return;
         }
         const uint16_t* kr = kb + kcol;
