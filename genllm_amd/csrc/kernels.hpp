@@ -75,6 +75,10 @@ struct AttnParams {
     // split-K decode: per-split partials [unit][split][row][D] then {m, l} per (unit, split, row)
     float* partial = nullptr;
     int32_t pages_per_split = 0, n_splits = 1, n_chunks = 1;
+    // Single-launch merge: per-kv-head arrival counters (zero between
+    // launches); the last split workgroup of a head to arrive merges them.
+    // nullptr = merge in a second kernel.
+    int32_t* counters = nullptr;
     // fused append (decode of the op): tokens at positions >= new_from are read
     // from k_new / v_new ([Hkv][S][D], strides in elements) instead of the
     // pools and written into the pools by the wave that reads their page; page
@@ -90,7 +94,11 @@ struct AttnParams {
     TableUpdate upd;
 };
 
-// Workspace layout of the split-K decode.
+// Workspace layout of the split-K decode: kDecodeCounterBytes of per-kv-head
+// arrival counters (must be zero before the first launch; every launch leaves
+// them at zero), then the per-split partials.
+constexpr size_t kDecodeCounterBytes = 1024;
+constexpr int kDecodeMaxKvHeads = int(kDecodeCounterBytes / sizeof(int32_t));
 size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages);
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws);
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream);

@@ -220,10 +220,15 @@ struct Append {
                 uint16_t* dst = is_q ? p.q_out + tok[u] * p.qo_tok_stride + h[u] * p.qo_head_stride
                                      : k_dst(p, tok[u], h[u]);
                 if (!dst) continue;
+                if (is_q) {  // q_out is read by the attention kernel right after: plain stores keep it cached
 #pragma unroll
-                for (int c = 0; c < R; ++c)
-                    __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x2, x[u][c]),
-                                                reinterpret_cast<nt_u32x2*>(dst + 4 * j + 32 * c));
+                    for (int c = 0; c < R; ++c) *reinterpret_cast<uint2*>(dst + 4 * j + 32 * c) = x[u][c];
+                } else {  // K page rows: not read again within the call
+#pragma unroll
+                    for (int c = 0; c < R; ++c)
+                        __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x2, x[u][c]),
+                                                    reinterpret_cast<nt_u32x2*>(dst + 4 * j + 32 * c));
+                }
             }
         } else {
             uint4 xv[TPW][U];

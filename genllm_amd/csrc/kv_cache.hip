@@ -63,6 +63,19 @@ struct BlockPool {
         if (capacity > 0 && num_blocks >= capacity) return -1;
         return num_blocks++;
     }
+    // alloc() that reports whether the id came off the free list, so that
+    // unalloc() can revert it: undone in reverse allocation order, the pool
+    // is restored exactly (free-list order included).
+    int32_t alloc(bool& from_free) {
+        from_free = !free_list.empty();
+        return alloc();
+    }
+    void unalloc(int32_t id, bool from_free) {
+        if (from_free)
+            free_list.push_back(id);
+        else
+            --num_blocks;
+    }
     void free(int32_t id) {
         if (id >= 0 && id < num_blocks) free_list.push_back(id);
     }
@@ -84,6 +97,9 @@ struct LayerState {
     std::vector<int32_t> k_ids, v_ids;  // page table
     uint16_t* k_base = nullptr;
     uint16_t* v_base = nullptr;
+    // Device page table: its own allocation (2 * max_blocks int32), outside
+    // the kv_cache pool, so that the pool holds exactly the K and V pools the
+    // scheduler sizes it for (scheduler.cpp:62-79).
     int32_t* d_k_ids = nullptr;
     int32_t* d_v_ids = nullptr;
     // Pinned host staging of the table ([max_blocks] K ids, then [max_blocks]
@@ -104,9 +120,13 @@ struct genllm_kv {
     char* base = nullptr;  // kv_cache MemoryPool buffer
     size_t capacity = 0, cursor = 0;
     std::map<int32_t, LayerState> layers;
-    void* ws = nullptr;    // split-K decode workspace (per-split partials)
+    // Split-K decode workspace (arrival counters, then per-split partials),
+    // sized by reserve_layer for the largest reserved layer and zero-filled
+    // there; the op path never allocates, frees or synchronises.
+    void* ws = nullptr;
     size_t ws_bytes = 0;
     std::vector<void*> pinned;     // every h_ids buffer, freed at destroy
+    std::vector<void*> tables;     // every device page table, freed at destroy
     bool uploads_pending = false;  // async table uploads from h_ids may be in flight
 };
 
@@ -137,36 +157,62 @@ int64_t pages_opened(int32_t num_cached, int32_t count) {
     return (int64_t(num_cached) + count + kPage - 1) / kPage - (int64_t(num_cached) + kPage - 1) / kPage;
 }
 
-// append_kv_pages (page_attention.cpp:141-162) on the host state.  New entries
-// go to the device table either through `upd` (the next kernel writes them;
-// when given and large enough) or with async copies on `stream` from the
-// layer's pinned staging.
+// What one append_pages call changed, so that a failure after it (a kernel
+// launch error) can restore the layer exactly.
+struct AppendUndo {
+    int32_t num_cached = 0;
+    size_t table_size = 0;
+    std::vector<std::pair<int32_t, bool>> k, v;  // ids handed out, and whether from the free list
+};
+
+// append_kv_pages (page_attention.cpp:141-162) on the host state, in closed
+// form: the positions g in [num_cached, num_cached + count) with g % 16 == 0
+// are the page indices first .. first + need - 1; each takes one K and one V
+// block, and enters the table only past its end (as the reference pushes).
+// Every check runs before the state changes, so an error leaves the layer
+// as it was.  New entries go to the device table either through `upd` (the
+// next kernel writes them; when given and large enough) or with async copies
+// on `stream` from the layer's pinned staging.
 template <typename Upd = TableUpdate>
-int append_pages(genllm_kv* kv, LayerState& s, int32_t count, hipStream_t stream, Upd* upd = nullptr) {
+int append_pages(genllm_kv* kv, LayerState& s, int32_t count, hipStream_t stream, Upd* upd = nullptr,
+                 AppendUndo* undo = nullptr) {
     constexpr size_t kCap = sizeof(Upd::k) / sizeof(int32_t);
     if (upd) *upd = Upd{};
+    if (undo) {
+        undo->num_cached = s.num_cached;
+        undo->table_size = s.k_ids.size();
+        undo->k.clear();
+        undo->v.clear();
+    }
     if (!s.active || count <= 0) return GENLLM_OK;
+    if (int64_t(s.num_cached) + count > int64_t(INT32_MAX) - kPage)
+        return fail(GENLLM_ERR_INVALID, "append_kv_pages: position overflow");
+    const int64_t first = (int64_t(s.num_cached) + kPage - 1) / kPage;
     const int64_t need = pages_opened(s.num_cached, count);
     if (need > s.k_pool.available() || need > s.v_pool.available())
         return fail(GENLLM_ERR_POOL_FULL, "append_kv_pages: block pool exhausted (" + std::to_string(need) +
                                               " pages needed)");
     const size_t old_size = s.k_ids.size();
-    for (int32_t p = 0; p < count; ++p) {
-        const int32_t g = s.num_cached + p;
-        if (g % kPage == 0) {
-            const int32_t k = s.k_pool.alloc();
-            const int32_t v = s.v_pool.alloc();
-            if (g / kPage >= int32_t(s.k_ids.size())) {
-                s.k_ids.push_back(k);
-                s.v_ids.push_back(v);
-            }
+    if (need > 0 && first > int64_t(old_size))
+        return fail(GENLLM_ERR_INVALID, "append_kv_pages: page table shorter than num_cached");
+    const size_t new_size = std::max<size_t>(old_size, size_t(first + need));
+    if (s.d_k_ids && new_size > size_t(s.max_blocks))
+        return fail(GENLLM_ERR_POOL_FULL, "append_kv_pages: page table longer than max_blocks");
+    for (int64_t i = 0; i < need; ++i) {
+        bool kf = false, vf = false;
+        const int32_t k = s.k_pool.alloc(kf);
+        const int32_t v = s.v_pool.alloc(vf);
+        if (undo) {
+            undo->k.emplace_back(k, kf);
+            undo->v.emplace_back(v, vf);
+        }
+        if (first + i >= int64_t(s.k_ids.size())) {
+            s.k_ids.push_back(k);
+            s.v_ids.push_back(v);
         }
     }
     s.num_cached += count;
-    const size_t new_size = s.k_ids.size();
     if (new_size > old_size && s.d_k_ids) {
-        if (new_size > size_t(s.max_blocks))
-            return fail(GENLLM_ERR_POOL_FULL, "append_kv_pages: page table longer than max_blocks");
         const size_t n = new_size - old_size;
         if (upd && n <= kCap) {
             upd->first = int32_t(old_size);
@@ -188,24 +234,43 @@ int append_pages(genllm_kv* kv, LayerState& s, int32_t count, hipStream_t stream
     return GENLLM_OK;
 }
 
+// Restores the layer to its state before the append_pages call `u` recorded.
+void undo_append(LayerState& s, const AppendUndo& u) {
+    for (size_t i = u.k.size(); i-- > 0;) {
+        s.k_pool.unalloc(u.k[i].first, u.k[i].second);
+        s.v_pool.unalloc(u.v[i].first, u.v[i].second);
+    }
+    s.k_ids.resize(u.table_size);
+    s.v_ids.resize(u.table_size);
+    s.num_cached = u.num_cached;
+}
+
+// Per-thread undo record (its vectors keep their capacity across calls).
+thread_local AppendUndo t_undo;
+
 LayerState* active_layer(genllm_kv* kv, int32_t layer) {
     auto it = kv->layers.find(layer);
     if (it == kv->layers.end() || !it->second.active) return nullptr;
     return &it->second;
 }
 
-// Split-K workspace sized for the layer's max_blocks, grown when a wider query
-// chunk needs more rows.
-int ensure_workspace(genllm_kv* kv, size_t need) {
+// Split-K workspace of the manager, grown at set-up only (reserve_layer) to
+// the largest decode plan any reserved layer can make: 16 rows per kv head
+// (the decode kernel's limit) and as many splits as the layer's max_blocks
+// allow.  The new buffer is zero-filled: its arrival counters must start at
+// zero, and the kernels leave them at zero.
+int reserve_workspace(genllm_kv* kv, size_t need) {
     if (need <= kv->ws_bytes) return GENLLM_OK;
+    GENLLM_HIP_TRY(hipSetDevice(kv->device));
     if (kv->ws) {
-        GENLLM_HIP_TRY(hipDeviceSynchronize());
+        GENLLM_HIP_TRY(hipDeviceSynchronize());  // the old buffer may still be in use
         GENLLM_HIP_TRY(hipFree(kv->ws));
         kv->ws = nullptr;
         kv->ws_bytes = 0;
     }
     GENLLM_HIP_TRY(hipMalloc(&kv->ws, need));
     kv->ws_bytes = need;
+    GENLLM_HIP_TRY(hipMemset(kv->ws, 0, need));
     return GENLLM_OK;
 }
 
@@ -239,18 +304,18 @@ int check_attn_args(const AttnParams& p, int head_dim) {
     return GENLLM_OK;
 }
 
-// Short query chunks (<= 16 rows per kv head) take the split-K decode kernel,
-// with the manager's workspace sized for the most splits the layer's largest
-// table can need; longer chunks take the MFMA prefill kernel.
-int run_attention(AttnParams p, int head_dim, int32_t max_blocks, hipStream_t stream, genllm_kv* kv) {
+// Short query chunks (<= 16 rows per kv head) take the split-K decode kernel
+// on the manager's workspace (reserve_layer sized it for every plan a reserved
+// layer can make); longer chunks take the MFMA prefill kernel.  Checks and the
+// split plan come first, so a caller can run them before changing any state.
+int prepare_attention(AttnParams& p, int head_dim, genllm_kv* kv) {
     if (int rc = check_attn_args(p, head_dim)) return rc;
-    if (p.G * p.S <= 16) {
-        const int ws_pages = std::max(p.n_pages, max_blocks);
-        const size_t need = decode_workspace_bytes(p.Hq, p.Hkv, p.S, head_dim, ws_pages);
-        if (int rc = ensure_workspace(kv, need)) return rc;
-        if (int rc = decode_plan(p, head_dim, kv->ws_bytes, kv->ws)) return rc;
-        return launch_paged_decode(p, head_dim, stream);
-    }
+    if (p.G * p.S <= 16) return decode_plan(p, head_dim, kv->ws_bytes, kv->ws);
+    return GENLLM_OK;
+}
+
+int launch_attention(const AttnParams& p, int head_dim, hipStream_t stream) {
+    if (p.G * p.S <= 16) return launch_paged_decode(p, head_dim, stream);
     return launch_paged_prefill(p, head_dim, stream);
 }
 
@@ -293,6 +358,7 @@ extern "C" int genllm_kv_destroy(genllm_kv* kv) {
     (void)hipDeviceSynchronize();
     if (kv->base) (void)hipFree(kv->base);
     if (kv->ws) (void)hipFree(kv->ws);
+    for (void* t : kv->tables) (void)hipFree(t);
     for (void* h : kv->pinned) (void)hipHostFree(h);
     delete kv;
     return GENLLM_OK;
@@ -319,20 +385,38 @@ extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max
     if (!s.active || !kv->base) return GENLLM_OK;  // page_attention.cpp:84
     const size_t bb = size_t(kPage) * s.n_kv_heads * s.head_dim * elem_size(s.dtype);
     const size_t total = size_t(max_blocks) * bb;
-    void *kp, *vp, *ki, *vi;
+    // The pool holds exactly the K and V pools (2 * max_blocks * block_bytes,
+    // the scheduler's sizing, scheduler.cpp:62-79 and 371); the device page
+    // table, its pinned staging and the decode workspace are allocated
+    // separately, once, here.
+    const size_t cursor0 = kv->cursor;
+    void *kp, *vp;
     if (int rc = pool_allocate(kv, total, 256, &kp)) return rc;
-    if (int rc = pool_allocate(kv, total, 256, &vp)) return rc;
-    if (int rc = pool_allocate(kv, size_t(max_blocks) * 4, 256, &ki)) return rc;
-    if (int rc = pool_allocate(kv, size_t(max_blocks) * 4, 256, &vi)) return rc;
-    void* staging = nullptr;
+    if (int rc = pool_allocate(kv, total, 256, &vp)) {
+        kv->cursor = cursor0;
+        return rc;
+    }
     GENLLM_HIP_TRY(hipSetDevice(kv->device));
-    GENLLM_HIP_TRY(hipHostMalloc(&staging, size_t(max_blocks) * 2 * sizeof(int32_t), hipHostMallocDefault));
+    void* table = nullptr;
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&table, size_t(max_blocks) * 2 * sizeof(int32_t));
+    if (e == hipSuccess) e = hipHostMalloc(&staging, size_t(max_blocks) * 2 * sizeof(int32_t), hipHostMallocDefault);
+    if (e != hipSuccess) {
+        if (table) (void)hipFree(table);
+        kv->cursor = cursor0;
+        return hip_fail(e, "reserve_layer: page table allocation");
+    }
+    kv->tables.push_back(table);
     kv->pinned.push_back(staging);
+    const int rows = 16;  // decode kernel limit: (query, q-head) rows per kv head
+    if (int rc = reserve_workspace(
+            kv, decode_workspace_bytes(rows * s.n_kv_heads, s.n_kv_heads, 1, s.head_dim, max_blocks)))
+        return rc;
     s.h_ids = static_cast<int32_t*>(staging);
     s.k_base = static_cast<uint16_t*>(kp);
     s.v_base = static_cast<uint16_t*>(vp);
-    s.d_k_ids = static_cast<int32_t*>(ki);
-    s.d_v_ids = static_cast<int32_t*>(vi);
+    s.d_k_ids = static_cast<int32_t*>(table);
+    s.d_v_ids = static_cast<int32_t*>(table) + max_blocks;
     s.block_bytes = bb;
     s.max_blocks = max_blocks;
     s.k_pool = BlockPool{};
@@ -466,15 +550,44 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     if (!aligned(k, 16) || !aligned(v, 16))
         return fail(GENLLM_ERR_INVALID, "paged_attention: k/v must be 16-byte aligned");
     hipStream_t st = as_stream(stream);
+    const int32_t pos0 = s->num_cached;
+    if (int64_t(pos0) + seq_len > int64_t(INT32_MAX) - kPage)
+        return fail(GENLLM_ERR_INVALID, "paged_attention: position overflow");
+    const int32_t n_after = pos0 + seq_len;
+    const bool fuse = int64_t(n_kv_groups) * seq_len <= 16;
+
+    // 0. attention arguments and split plan for the state after the append,
+    // checked before anything changes: an error leaves the layer as it was
+    AttnParams p;
+    p.q = static_cast<const uint16_t*>(q);
+    p.q_head_stride = int64_t(seq_len) * head_dim;
+    p.q_tok_stride = head_dim;
+    p.out = static_cast<uint16_t*>(out);
+    p.o_head_stride = int64_t(seq_len) * head_dim;
+    p.o_tok_stride = head_dim;
+    p.k_pool = s->k_base;
+    p.v_pool = s->v_base;
+    p.k_ids = s->d_k_ids;
+    p.v_ids = s->d_v_ids;
+    p.n_cached = n_after;
+    p.n_pages = (n_after + kPage - 1) / kPage;
+    p.S = seq_len;
+    p.Hq = n_q_heads;
+    p.Hkv = n_kv_heads;
+    p.G = n_kv_groups;
+    p.scale_log2 = scale * kLog2e;
+    p.causal = causal != 0;
+    p.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
+    p.kv_row = int64_t(n_kv_heads) * head_dim;
+    if (int rc = prepare_attention(p, head_dim, kv)) return rc;
 
     // 1. append (append_kv_from_tensor, attention.cpp:146): head-major [Hkv][S][D].
     // Short chunks (the decode kernel's range) append inside the attention
     // kernel itself: the wave that reads a page takes the new rows from k/v and
     // writes them to their slots, so no separate launch is needed.
-    const int32_t pos0 = s->num_cached;
-    const bool fuse = int64_t(n_kv_groups) * seq_len <= 16;
     AppendParams ap;
-    if (int rc = append_pages(kv, *s, seq_len, st, &ap.upd)) return rc;
+    AppendUndo& undo = t_undo;
+    if (int rc = append_pages(kv, *s, seq_len, st, &ap.upd, &undo)) return rc;
     ap.k = static_cast<const uint16_t*>(k);
     ap.v = static_cast<const uint16_t*>(v);
     ap.k_tok_stride = ap.v_tok_stride = head_dim;
@@ -489,32 +602,14 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     ap.k_ids = s->d_k_ids;
     ap.v_ids = s->d_v_ids;
     ap.max_blocks = s->max_blocks;
-    if (!fuse)
-        if (int rc = launch_kv_append(ap, head_dim, st)) return rc;
-    if (s->k_ids.empty()) return GENLLM_OK;  // attention.cpp:148
+    if (!fuse) {
+        if (int rc = launch_kv_append(ap, head_dim, st)) {
+            undo_append(*s, undo);
+            return rc;
+        }
+    }
 
     // 2. attend over all cached tokens
-    AttnParams p;
-    p.q = static_cast<const uint16_t*>(q);
-    p.q_head_stride = int64_t(seq_len) * head_dim;
-    p.q_tok_stride = head_dim;
-    p.out = static_cast<uint16_t*>(out);
-    p.o_head_stride = int64_t(seq_len) * head_dim;
-    p.o_tok_stride = head_dim;
-    p.k_pool = s->k_base;
-    p.v_pool = s->v_base;
-    p.k_ids = s->d_k_ids;
-    p.v_ids = s->d_v_ids;
-    p.n_cached = s->num_cached;
-    p.n_pages = std::min<int32_t>(int32_t(s->k_ids.size()), (s->num_cached + kPage - 1) / kPage);
-    p.S = seq_len;
-    p.Hq = n_q_heads;
-    p.Hkv = n_kv_heads;
-    p.G = n_kv_groups;
-    p.scale_log2 = scale * kLog2e;
-    p.causal = causal != 0;
-    p.page_elems = ap.page_elems;
-    p.kv_row = int64_t(n_kv_heads) * head_dim;
     if (fuse) {
         p.k_new = ap.k;
         p.v_new = ap.v;
@@ -525,9 +620,9 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
         p.v_pool_w = s->v_base;
         p.k_ids_w = s->d_k_ids;
         p.v_ids_w = s->d_v_ids;
-        // seq_len <= 16 opens at most 2 pages
-        if (ap.upd.count > int32_t(sizeof(p.upd.k) / sizeof(int32_t)))
-            return fail(GENLLM_ERR_INVALID, "paged_attention: too many pages opened for the fused append");
+        // seq_len <= 16 opens at most 2 pages, which fit the launch arguments
+        // (append_pages put them in ap.upd, as it holds up to 256)
+        static_assert(sizeof(p.upd.k) / sizeof(int32_t) >= 2, "decode step opens up to 2 pages");
         p.upd.first = ap.upd.first;
         p.upd.count = ap.upd.count;
         for (int32_t i = 0; i < ap.upd.count; ++i) {
@@ -535,7 +630,11 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
             p.upd.v[i] = ap.upd.v[i];
         }
     }
-    return run_attention(p, head_dim, s->max_blocks, st, kv);
+    if (int rc = launch_attention(p, head_dim, st)) {
+        if (fuse) undo_append(*s, undo);  // nothing ran: the fused append is part of this launch
+        return rc;
+    }
+    return GENLLM_OK;
 }
 
 extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t seq_len, const void* k,
@@ -569,7 +668,8 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     hipStream_t st = as_stream(stream);
     AppendParams ap;
     const int32_t pos0 = s->num_cached;
-    if (int rc = append_pages(kv, *s, seq_len, st, &ap.upd)) return rc;
+    AppendUndo& undo = t_undo;
+    if (int rc = append_pages(kv, *s, seq_len, st, &ap.upd, &undo)) return rc;
     ap.k = static_cast<const uint16_t*>(k);
     ap.k_tok_stride = k_tok_stride;
     ap.k_head_stride = k_head_stride;
@@ -602,7 +702,11 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     ap.k_ids = s->d_k_ids;
     ap.v_ids = s->d_v_ids;
     ap.max_blocks = s->max_blocks;
-    return launch_kv_append(ap, D, st);
+    if (int rc = launch_kv_append(ap, D, st)) {
+        undo_append(*s, undo);
+        return rc;
+    }
+    return GENLLM_OK;
 }
 
 // ---------------------------------------------------------- stateless ops

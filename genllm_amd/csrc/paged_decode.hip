@@ -42,6 +42,7 @@
 // needs agent-scope fences -- an L2 write-back and invalidate per workgroup on
 // gfx950 -- and measured slower.)
 #include <cfloat>
+#include <string>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -61,11 +62,137 @@ constexpr int kMaxSplits = 256;
 template <int D>
 constexpr int kPagesInFlight = D == 128 ? 1 : 2;
 constexpr int VT_ROW = kPage + 4;  // LDS V^T row: 16 tokens + pad (bf16 elements)
-constexpr int kNonTemporal = 2;    // buffer-load cache policy bit nt (gfx950: sc0 = 1, nt = 2, sc1 = 16)
+constexpr int kNonTemporal = 2;    // buffer-access cache policy bit nt (gfx950: sc0 = 1, nt = 2, sc1 = 16)
+// Cache policy sc1 (agent scope): a store completes at the device's coherence
+// point and a load reads from it, past the XCD-local caches.  This is what the
+// compiler emits for relaxed agent-scope atomic stores and loads on gfx950.
+constexpr int kCoherent = 16;
+typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
     const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
     return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+// Buffer resource over the split partials: o [Hkv][split][row][D], then
+// {m, l} [Hkv][split][row].
+template <int D>
+__device__ __forceinline__ auto part_rsrc(const AttnParams& p) {
+    const int rows = p.G * p.S;
+    const int bytes = int(int64_t(p.Hkv) * p.n_splits * rows * (D + 2) * 4);
+    return __builtin_amdgcn_make_buffer_rsrc(p.partial, 0, bytes, kBufferFlags);
+}
+
+// Single-launch merge, run by every split workgroup after it has stored its
+// partial (sc1): the workgroup counts its arrival on its kv head, and the last
+// one to arrive merges all splits of that head with the log-sum-exp rule
+//   M = max m_s, L = sum l_s 2^(m_s-M), O = sum o_s 2^(m_s-M), out = O * (1/L)
+// and resets the counter for the next launch.  Ordering: each wave waits for
+// its own partial stores to complete (vmcnt(0)) before the barrier that
+// precedes the count, and the last workgroup loads the partials only after the
+// count has returned, from the coherence point (sc1) -- so no L2 write-back or
+// invalidate is needed.  Merge work: W waves over (row, split) pairs -- for
+// R < W rows, W/R waves share a row's splits -- with up to kMergeU splits in
+// flight per lane, then the per-wave states meet in LDS.
+template <int D, int W>
+__device__ __forceinline__ void merge_last_arrival(const AttnParams& p, int h, float (&lds_m)[W][kRows],
+                                                   float (&lds_l)[W][kRows], float (&lds_o)[W][kRows][D + 4]) {
+    constexpr int VH = D / 128;
+    constexpr int U = kMergeU;
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int R = p.G * p.S, ns = p.n_splits;
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(p.counters + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == ns - 1;
+        if (last) __hip_atomic_store(p.counters + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    const auto rs = part_rsrc<D>(p);
+    const int64_t ml_base = int64_t(p.Hkv) * ns * R * D;  // float index of {m, l}
+    const int wpr = R < W ? W / R : 1;                     // waves per row
+    const int sub = wv % wpr;
+    for (int r = wv / wpr; r < R; r += W / wpr) {
+        float mw = -INFINITY, lw = 0.0f, o0[VH], o1[VH];
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh) o0[hh] = o1[hh] = 0.0f;
+        for (int s0 = sub; s0 < ns; s0 += wpr * U) {
+            float2 ov[U][VH], mv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s2 = s0 + wpr * u;
+                const int64_t row = (int64_t(h) * ns + s2) * R + r;
+#pragma unroll
+                for (int hh = 0; hh < VH; ++hh)
+                    ov[u][hh] = s2 < ns ? __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                         rs, int(4 * (row * D + 128 * hh + 2 * lane)),
+                                                                         0, kCoherent))
+                                        : make_float2(0.0f, 0.0f);
+                mv[u] = s2 < ns ? __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                 rs, int(4 * (ml_base + 2 * row)), 0, kCoherent))
+                                : make_float2(-INFINITY, 0.0f);
+            }
+            float bm = mw;
+#pragma unroll
+            for (int u = 0; u < U; ++u) bm = fmaxf(bm, mv[u].x);
+            if (bm == -INFINITY) continue;  // nothing visible yet
+            const float a = mw == -INFINITY ? 0.0f : exp2_fast(mw - bm);
+            lw *= a;
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh) {
+                o0[hh] *= a;
+                o1[hh] *= a;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float w = mv[u].x == -INFINITY ? 0.0f : exp2_fast(mv[u].x - bm);
+                lw += mv[u].y * w;
+#pragma unroll
+                for (int hh = 0; hh < VH; ++hh) {
+                    o0[hh] += ov[u][hh].x * w;
+                    o1[hh] += ov[u][hh].y * w;
+                }
+            }
+            mw = bm;
+        }
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh) {
+            lds_o[sub][r][128 * hh + 2 * lane] = o0[hh];
+            lds_o[sub][r][128 * hh + 2 * lane + 1] = o1[hh];
+        }
+        if (lane == 0) {
+            lds_m[sub][r] = mw;
+            lds_l[sub][r] = lw;
+        }
+    }
+    __syncthreads();
+    for (int r = wv; r < R; r += W) {
+        float M = -INFINITY;
+        for (int w2 = 0; w2 < wpr; ++w2) M = fmaxf(M, lds_m[w2][r]);
+        float L = 0.0f, O0[VH], O1[VH];
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh) O0[hh] = O1[hh] = 0.0f;
+        for (int w2 = 0; w2 < wpr; ++w2) {
+            const float e = lds_m[w2][r] == -INFINITY ? 0.0f : exp2_fast(lds_m[w2][r] - M);
+            L += lds_l[w2][r] * e;
+#pragma unroll
+            for (int hh = 0; hh < VH; ++hh) {
+                O0[hh] += lds_o[w2][r][128 * hh + 2 * lane] * e;
+                O1[hh] += lds_o[w2][r][128 * hh + 2 * lane + 1] * e;
+            }
+        }
+        const float inv = 1.0f / L;
+        uint16_t* orow = p.out + int64_t(h * p.G + r % p.G) * p.o_head_stride + int64_t(r / p.G) * p.o_tok_stride;
+#pragma unroll
+        for (int hh = 0; hh < VH; ++hh)
+            *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
+                pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
+    }
 }
 
 template <int D>
@@ -354,17 +481,27 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
                 *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
                     pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
         } else {
-            // partials: o [h][split][row][D], then {m, l} [h][split][row]
-            float* po = p.partial + ((int64_t(h) * p.n_splits + sp) * rows_total + ri) * D;
+            // partials: o [h][split][row][D], then {m, l} [h][split][row].
+            // With the in-kernel merge they are stored agent-coherent (sc1:
+            // the store completes at the device's coherence point, not in this
+            // XCD's L2), so no cache write-back is needed before the arrival
+            // count below.
+            const int64_t o_off = ((int64_t(h) * p.n_splits + sp) * rows_total + ri) * D;
+            const int64_t ml_off = int64_t(p.Hkv) * p.n_splits * rows_total * D +
+                                   2 * ((int64_t(h) * p.n_splits + sp) * rows_total + ri);
+            const auto rs = part_rsrc<D>(p);
+            auto store = [&](float2 v, int64_t at) {  // at: float index
+                if (p.counters)
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, v), rs, int(4 * at), 0, kCoherent);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, v), rs, int(4 * at), 0, 0);
+            };
 #pragma unroll
-            for (int hh = 0; hh < VH; ++hh)
-                *reinterpret_cast<float2*>(po + 128 * hh + 2 * lane) = make_float2(O0[hh], O1[hh]);
-            if (lane == 0) {
-                float2* ml = reinterpret_cast<float2*>(p.partial + int64_t(p.Hkv) * p.n_splits * rows_total * D);
-                ml[(int64_t(h) * p.n_splits + sp) * rows_total + ri] = make_float2(M, L);
-            }
+            for (int hh = 0; hh < VH; ++hh) store(make_float2(O0[hh], O1[hh]), o_off + 128 * hh + 2 * lane);
+            if (lane == 0) store(make_float2(M, L), ml_off);
         }
     }
+    if (p.counters && p.n_splits > 1) merge_last_arrival<D, W>(p, h, lds_m, lds_l, lds_o);
 }
 
 // Merge of the splits: one workgroup of MW waves per (kv head, row), grid
@@ -472,7 +609,20 @@ size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages) {
     if (Hkv <= 0 || Hq <= 0 || S <= 0 || D <= 0 || n_pages <= 0) return 0;
     const size_t rows = size_t(Hq / Hkv) * S;
     const size_t splits = std::min<size_t>(size_t(n_pages), kMaxSplits);
-    return size_t(Hkv) * splits * rows * (D + 2) * sizeof(float);
+    return kDecodeCounterBytes + size_t(Hkv) * splits * rows * (D + 2) * sizeof(float);
+}
+
+// The split merge runs in a second kernel unless GENLLM_DECODE_MERGE=fused
+// asks for the single-launch form (the last workgroup of each kv head to
+// finish merges it).  Measured at config 3 (MI355X, 400 back-to-back launches
+// over 16 rotating layers): two kernels 12.7 us per decode (split 10.3 us +
+// merge 3.7 us in the kernel trace), single launch 14.6 us (14.45 us kernel):
+// the last workgroup's serial tail -- coherent stores completing, the arrival
+// count, then coherent loads of every partial -- costs more than the second
+// launch.
+static bool merge_in_split_kernel() {
+    const char* e = getenv("GENLLM_DECODE_MERGE");
+    return e && std::string(e) == "fused";
 }
 
 // Pages per split: about GENLLM_DECODE_WG_PER_CU (default 1) workgroups per CU
@@ -494,12 +644,18 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
     pps = std::min(pps, 64 * kWaves);  // a wave holds the ids of at most 64 pages
     p.pages_per_split = pps;
     p.n_splits = (p.n_pages + pps - 1) / pps;
+    p.partial = nullptr;
+    p.counters = nullptr;
     if (p.n_splits > 1) {
-        const size_t need = size_t(p.Hkv) * p.n_splits * (p.G * p.S) * (D + 2) * sizeof(float);
+        if (p.Hkv > kDecodeMaxKvHeads)
+            return fail(GENLLM_ERR_UNSUPPORTED, "paged decode: at most 256 kv heads");
+        const size_t need =
+            kDecodeCounterBytes + size_t(p.Hkv) * p.n_splits * (p.G * p.S) * (D + 2) * sizeof(float);
         if (!ws || ws_bytes < need)
             return fail(GENLLM_ERR_INVALID, "paged decode: workspace too small (need " + std::to_string(need) +
                                                 " bytes, have " + std::to_string(ws_bytes) + ")");
-        p.partial = static_cast<float*>(ws);
+        p.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kDecodeCounterBytes);
+        if (merge_in_split_kernel()) p.counters = static_cast<int32_t*>(ws);
     }
     return GENLLM_OK;
 }
@@ -516,7 +672,7 @@ int launch_decode_d(const AttnParams& p, hipStream_t stream) {
     if (!wide)
         hipLaunchKernelGGL((paged_decode_kernel<D, kWaves>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64), 0, stream, p);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
-    if (p.n_splits > 1) {
+    if (p.n_splits > 1 && !p.counters) {
         if (p.n_splits > 4 * kMergeU)
             hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), dim3(p.Hkv, p.G * p.S), dim3(8 * 64), 0, stream, p);
         else

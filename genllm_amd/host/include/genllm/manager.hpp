@@ -33,10 +33,18 @@ public:
     void set_stream(Device dev, size_t dev_id, void* stream);
     void* stream(Device dev, size_t dev_id) const;
 
+    // Device scratch of the ops that need one (the GEMM path of LinearImpl
+    // with a bias), reserved before execution -- size it with
+    // op_workspace_bytes -- so that no op allocates, frees or synchronises.
+    // Growing it waits for the device and replaces the buffer.
+    void reserve_op_workspace(Device dev, size_t dev_id, size_t bytes);
+    void* op_workspace(Device dev, size_t dev_id, size_t* bytes) const;
+
 private:
     using DevKey = std::pair<Device, size_t>;
     std::map<DevKey, std::unique_ptr<PagedAttentionManager>> attention_managers_;
     std::map<DevKey, void*> streams_;
+    std::map<DevKey, std::pair<void*, size_t>> workspaces_;
 };
 
 extern MemoryManager* g_mem_manager;
@@ -48,6 +56,10 @@ extern MemoryManager* g_mem_manager;
 // kv_cache_per_layer = 0 configuration) own no pages.
 size_t kv_cache_bytes(const std::vector<Tensor*>& nodes, Device dev, int32_t max_seq_len, float pool_factor = 1.0f);
 void initialize_kv_cache(PagedAttentionManager& pam, const std::vector<Tensor*>& nodes, int32_t max_seq_len);
+
+// Op workspace the nodes of `dev` need with up to max_rows rows (tokens) per
+// call: the largest genllm_linear_workspace_bytes over its LINEAR nodes.
+size_t op_workspace_bytes(const std::vector<Tensor*>& nodes, Device dev, int64_t max_rows);
 
 // README.md:97 -- kv_cache_per_layer: 0 = standard attention, >= 1 = paged
 // attention; the op type an attention node is built with.

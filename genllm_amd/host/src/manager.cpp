@@ -3,7 +3,13 @@
 // 404-430).
 #include "genllm/manager.hpp"
 
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
 #include <stdexcept>
+#include <string>
+
+#include "genllm_paged.h"
 
 MemoryManager* g_mem_manager = nullptr;
 
@@ -11,6 +17,11 @@ MemoryManager::MemoryManager() { g_mem_manager = this; }
 
 MemoryManager::~MemoryManager() {
     attention_managers_.clear();
+    for (auto& [key, ws] : workspaces_)
+        if (ws.first && hipSetDevice(int(key.second)) == hipSuccess) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(ws.first);
+        }
     if (g_mem_manager == this) g_mem_manager = nullptr;
 }
 
@@ -43,6 +54,28 @@ void* MemoryManager::stream(Device dev, size_t dev_id) const {
     return it == streams_.end() ? nullptr : it->second;
 }
 
+void MemoryManager::reserve_op_workspace(Device dev, size_t dev_id, size_t bytes) {
+    if (dev != Device::HIP) throw std::runtime_error("reserve_op_workspace: this library manages HIP devices only");
+    auto& ws = workspaces_[{dev, dev_id}];
+    if (bytes <= ws.second) return;
+    if (hipSetDevice(int(dev_id)) != hipSuccess) throw std::runtime_error("reserve_op_workspace: hipSetDevice failed");
+    if (ws.first) {
+        if (hipDeviceSynchronize() != hipSuccess || hipFree(ws.first) != hipSuccess)
+            throw std::runtime_error("reserve_op_workspace: releasing the old workspace failed");
+        ws = {nullptr, 0};
+    }
+    if (hipMalloc(&ws.first, bytes) != hipSuccess)
+        throw std::runtime_error("reserve_op_workspace: allocation of " + std::to_string(bytes) + " bytes failed");
+    ws.second = bytes;
+}
+
+void* MemoryManager::op_workspace(Device dev, size_t dev_id, size_t* bytes) const {
+    auto it = workspaces_.find({dev, dev_id});
+    const bool have = it != workspaces_.end();
+    if (bytes) *bytes = have ? it->second.second : 0;
+    return have ? it->second.first : nullptr;
+}
+
 // ------------------------------------------------------------- scheduler
 namespace {
 int32_t max_blocks_for(int32_t max_seq_len) { return (max_seq_len + PAGE_BLOCK_SIZE - 1) / PAGE_BLOCK_SIZE; }
@@ -68,4 +101,16 @@ void initialize_kv_cache(PagedAttentionManager& pam, const std::vector<Tensor*>&
         pam.init_layer(t->layer_id, int32_t(t->src[1]->dims[1]), int32_t(t->dims[3]), t->dtype);
         pam.reserve_layer(t->layer_id, max_blocks);
     }
+}
+
+size_t op_workspace_bytes(const std::vector<Tensor*>& nodes, Device dev, int64_t max_rows) {
+    size_t need = 0;
+    for (const Tensor* t : nodes) {
+        if (t->op_type != OperationType::OP_TYPE_LINEAR || t->device != dev || !t->src[0] || !t->src[1]) continue;
+        const bool bias = t->src[2] && t->src[2]->data;
+        if (!bias) continue;  // without a bias the GEMM rounds straight into the output
+        const int64_t common = t->src[0]->dims[2], cols = t->src[1]->dims[0];
+        need = std::max(need, genllm_linear_workspace_bytes(max_rows, common, cols));
+    }
+    return need;
 }

@@ -146,22 +146,17 @@ void LinearImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     const void* bp = bias && bias->data ? bias->data : nullptr;
     if (bp) require_bf16(bias, "linear");
     void* stream = device_stream(out, dev_id);
-    // fp32 workspace of the GEMM path, grown on demand; the old buffer is freed
-    // only after the stream has finished with it
-    static std::map<int32_t, std::pair<void*, size_t>> workspaces;
-    const size_t need = genllm_linear_workspace_bytes(rows, common, cols);
-    auto& ws = workspaces[dev_id];
-    if (need > ws.second) {
-        if (ws.first) {
-            if (hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess || hipFree(ws.first) != hipSuccess)
-                throw std::runtime_error("linear: releasing the old workspace failed");
-            ws = {nullptr, 0};
-        }
-        if (hipMalloc(&ws.first, need) != hipSuccess) throw std::runtime_error("linear: workspace allocation failed");
-        ws.second = need;
-    }
-    genllm_check(genllm_linear(x->data, w->data, bp, out->data, rows, common, cols, ws.first, ws.second, stream),
-                 "linear");
+    // fp32 workspace of the GEMM path with a bias: the device's op workspace,
+    // reserved before execution (MemoryManager::reserve_op_workspace); the op
+    // itself never allocates
+    const size_t need = bp ? genllm_linear_workspace_bytes(rows, common, cols) : 0;  // used only with a bias
+    size_t have = 0;
+    void* ws = g_mem_manager ? g_mem_manager->op_workspace(out->device, size_t(dev_id), &have) : nullptr;
+    if (need > have)
+        throw std::runtime_error("linear: this call needs " + std::to_string(need) +
+                                 " bytes of op workspace, the device has " + std::to_string(have) +
+                                 " reserved (MemoryManager::reserve_op_workspace, op_workspace_bytes)");
+    genllm_check(genllm_linear(x->data, w->data, bp, out->data, rows, common, cols, ws, have, stream), "linear");
 }
 
 }  // namespace ops

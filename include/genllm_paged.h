@@ -58,8 +58,12 @@ int genllm_kv_destroy(genllm_kv *kv);
 /* PagedAttentionManager::init_layer, src/core/page_attention.cpp:72-79 */
 int genllm_kv_init_layer(genllm_kv *kv, int32_t layer, int32_t n_kv_heads, int32_t head_dim, int32_t dtype);
 /* PagedAttentionManager::reserve_layer, page_attention.cpp:81-101: carves the
- * K pool, the V pool and the device page table (max_blocks entries) from the
- * kv_cache pool. */
+ * K pool and the V pool (max_blocks pages each, 256-byte aligned) from the
+ * kv_cache pool -- exactly the 2 * max_blocks * block_bytes per layer the
+ * reference scheduler sizes it for (scheduler.cpp:62-79, 371).  The device
+ * page table (max_blocks entries), its pinned host staging and the manager's
+ * decode workspace are allocated separately, here, once: the op itself never
+ * allocates, frees or synchronises. */
 int genllm_kv_reserve_layer(genllm_kv *kv, int32_t layer, int32_t max_blocks);
 /* PagedAttentionManager::is_active, page_attention.h:82-85; *active = 0/1 */
 int genllm_kv_is_active(genllm_kv *kv, int32_t layer, int32_t *active);
@@ -113,7 +117,10 @@ int genllm_kv_block_free(genllm_kv *kv, int32_t layer, int32_t which, int32_t id
  * and 256 (Qwen3.5, Qwen35.hpp:14-16) are served; any other returns
  * GENLLM_ERR_UNSUPPORTED (the CUDA op throws for head_dim != 128,
  * attention.cu:511).  Chunks of up to 16 (query, q-head) rows per kv head run
- * the split-K decode kernel, longer chunks the MFMA prefill kernel. */
+ * the split-K decode kernel, longer chunks the MFMA prefill kernel.  Every
+ * argument check and the split plan run before the layer changes: a call that
+ * returns an error leaves num_cached, the page tables and the block pools as
+ * they were. */
 int genllm_paged_attention(genllm_kv *kv, int32_t layer, const void *q, const void *k, const void *v, void *out,
                            int32_t batch, int32_t n_q_heads, int32_t seq_len, int32_t head_dim,
                            int32_t n_kv_heads, int32_t n_kv_groups, float scale, int32_t causal, void *stream);
@@ -167,15 +174,20 @@ int genllm_kv_scatter(const void *k, int64_t k_tok_stride, int64_t k_head_stride
                       const int32_t *k_ids, const int32_t *v_ids, int32_t pos0, int32_t seq_len,
                       int32_t n_kv_heads, int32_t head_dim, void *stream);
 
-/* Workspace for genllm_paged_decode: fp32 partial (m, l, o) per split (at most
- * 256 splits).  Two launches sharing a workspace must be ordered (same stream). */
+/* Workspace for genllm_paged_decode: 1 KiB of per-kv-head arrival counters,
+ * then fp32 partial (m, l, o) per split (at most 256 splits).  Zero-fill it
+ * once before its first use (the counters must start at zero; every launch
+ * leaves them at zero again).  Two launches sharing a workspace must be
+ * ordered (same stream). */
 size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int32_t seq_len,
                                            int32_t head_dim, int32_t max_pages);
 
 /* The attention loop of PagedAttentionImpl (attention.cpp:148-215) for short
  * query chunks (seq_len * n_q_heads / n_kv_heads <= 16 rows per kv head):
  * split-K over pages, GQA rows packed per kv head, then a log-sum-exp merge of
- * the splits by a second kernel on the same stream.  q/out rows addressed as base + h*head_stride + s*tok_stride
+ * the splits by a second kernel on the same stream (or, with
+ * GENLLM_DECODE_MERGE=fused, in the same launch by the last split of each kv
+ * head to finish).  q/out rows addressed as base + h*head_stride + s*tok_stride
  * (elements).  n_cached = total_cached; query s sits at n_cached - seq_len + s. */
 int genllm_paged_decode(const void *q, int64_t q_head_stride, int64_t q_tok_stride, void *out,
                         int64_t o_head_stride, int64_t o_tok_stride, const void *k_pool, const void *v_pool,

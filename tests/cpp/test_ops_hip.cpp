@@ -210,7 +210,8 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
         nodes[l].layer_id = l;
         graph.push_back(&nodes[l]);
     }
-    const size_t bytes = kv_cache_bytes(graph, Device::HIP, max_seq) + (1 << 20);
+    // exactly the scheduler's sizing, no slack (scheduler.cpp:62-79, 371)
+    const size_t bytes = kv_cache_bytes(graph, Device::HIP, max_seq);
     PagedAttentionManager& pam = mm.create_attention_manager(Device::HIP, 0, bytes);
     initialize_kv_cache(pam, graph, max_seq);
 
@@ -385,6 +386,18 @@ bool run_linear(int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_
     out.op_type = OperationType::OP_TYPE_LINEAR;
     out.src = {&X, &W, with_bias ? &Bv : nullptr, nullptr, nullptr, nullptr};
     out.op_params = {1.0f, 0, 0, 0};  // transpose_w
+    const size_t ws = op_workspace_bytes({&out}, Device::HIP, M);
+    if (ws > 0) {
+        // the op never allocates: without the reserved workspace it refuses
+        bool threw = false;
+        try {
+            kernel::dispatch(&out, 0);
+        } catch (const std::runtime_error&) {
+            threw = true;
+        }
+        ASSERT(threw, "linear GEMM with a bias refuses to run without a reserved op workspace");
+        mm.reserve_op_workspace(Device::HIP, 0, ws);
+    }
     ASSERT(kernel::dispatch(&out, 0), "executor dispatches LINEAR");
     std::vector<uint16_t> want(size_t(M * cols));
     or_linear_bf16(want.data(), hx.data(), hw.data(), M, common, cols, with_bias ? hb.data() : nullptr);

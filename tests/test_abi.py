@@ -57,9 +57,10 @@ def test_errors_are_reported():
 
 def test_decode_workspace_closed_form():
     L = _lib.lib()
-    # partials: Hkv x splits x rows (= groups * seq_len) x (D+2) fp32, splits <= min(pages, 256)
+    # 1 KiB of per-kv-head arrival counters, then partials: Hkv x splits x rows
+    # (= groups * seq_len) x (D+2) fp32, splits <= min(pages, 256)
     for Hq, Hkv, S, D, pages in [(32, 8, 1, 128, 513), (16, 8, 1, 128, 64), (32, 8, 3, 128, 10)]:
         rows = Hq // Hkv * S
-        want = Hkv * min(pages, 256) * rows * (D + 2) * 4
+        want = 1024 + Hkv * min(pages, 256) * rows * (D + 2) * 4
         assert L.genllm_paged_decode_workspace_bytes(Hq, Hkv, S, D, pages) == want
     assert L.genllm_paged_decode_workspace_bytes(0, 8, 1, 128, 4) == 0

@@ -47,26 +47,28 @@ class Context:
         self.info = self.mgr.get_layer(0)
         self.n_ctx = n_ctx
 
-    def decode(self, q_bits, causal=True, pps=None):
+    def decode(self, q_bits, causal=True, pps=None, merge=None):
         Hq, S, D = q_bits.shape
         out = torch.zeros((Hq, S, D), dtype=torch.bfloat16, device="cuda")
         n_pages = (self.n_ctx + 15) // 16
         ws = torch.zeros(paged.decode_workspace_bytes(Hq, self.Hkv, S, D, n_pages), dtype=torch.uint8,
                          device="cuda")
-        old = os.environ.get("GENLLM_DECODE_PPS")
+        saved = {k: os.environ.get(k) for k in ("GENLLM_DECODE_PPS", "GENLLM_DECODE_MERGE")}
         if pps:
             os.environ["GENLLM_DECODE_PPS"] = str(pps)
+        if merge:
+            os.environ["GENLLM_DECODE_MERGE"] = merge
         try:
             info = self.info
             paged.paged_decode(paged.to_device_bf16(q_bits), out, info.k_pool, info.v_pool, info.k_ids, info.v_ids,
                                n_pages, self.n_ctx, self.Hkv, scale_for(D), ws, causal=causal)
             torch.cuda.synchronize()
         finally:
-            if pps:
-                if old is None:
-                    del os.environ["GENLLM_DECODE_PPS"]
+            for k, v in saved.items():
+                if v is None:
+                    os.environ.pop(k, None)
                 else:
-                    os.environ["GENLLM_DECODE_PPS"] = old
+                    os.environ[k] = v
         return paged.to_host_bits(out), ws
 
     def oracle(self, q_bits, causal=True):
@@ -178,4 +180,24 @@ def test_decode_multi_query_head_dim_256(orc, S, causal):
     q = synth.normal_bf16(3400 + S, (8, S, 256))
     got, _ = ctx.decode(q, causal=causal)
     assert_attn_close(got, ctx.oracle(q, causal), f"D256 S{S} causal{causal}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,N,S,pps", [(32, 8, 128, 8193, 1, None), (32, 8, 128, 4100, 1, 64),
+                                            (16, 8, 128, 1000, 8, 3), (8, 2, 256, 4099, 1, None)])
+def test_decode_single_launch_merge(orc, Hq, Hkv, D, N, S, pps):
+    """GENLLM_DECODE_MERGE=fused: the last split workgroup of each kv head
+    merges the head's splits in the same launch (arrival counters in the
+    workspace).  Against the oracle, with the counters back at zero after the
+    launch (what makes a workspace reusable), and the default two-kernel merge
+    on the same inputs."""
+    pool = (N + 15) // 16 + 3
+    ctx = Context(orc, Hkv, D, pool, N, 7000 + N + S, nan_tail=True)
+    q = synth.normal_bf16(7100 + N, (Hq, S, D))
+    ref = ctx.oracle(q)
+    got, ws = ctx.decode(q, pps=pps, merge="fused")
+    assert_attn_close(got, ref, f"fused merge Hq{Hq} Hkv{Hkv} D{D} N{N} S{S}")
+    assert not ws[:1024].any().item(), "arrival counters not back at zero"
+    two, _ = ctx.decode(q, pps=pps)
+    assert_attn_close(two, ref, "two-kernel merge")
     ctx.close()

@@ -184,3 +184,71 @@ def test_op_qwen35_prefill_decode_sequence(orc):
     assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0))
     assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1))
     mgr.close()
+
+
+def layer_snapshot(mgr, layer):
+    """Host state, device page table and pool counters of a layer."""
+    i = mgr.get_layer(layer)
+    kt, vt = mgr.page_table(layer)
+    dk, dv = mgr.read_device_table(layer)
+    return (i.num_cached, i.num_pages, i.k_num_blocks, i.k_num_free, i.v_num_blocks, i.v_num_free,
+            kt.tolist(), vt.tolist(), dk.tolist(), dv.tolist())
+
+
+@pytest.mark.parametrize("S", [1, 40])
+def test_op_errors_leave_layer_unchanged(orc, S):
+    """A call the op refuses (misaligned q, NaN scale, a head-count mismatch)
+    changes nothing: num_cached, the host and device page tables and the block
+    pools are as before, and the next valid call matches the oracle.  Decode
+    (S = 1, the fused append) and prefill (S = 40, separate append kernel)."""
+    D, Hkv, Hq = 128, 8, 32
+    mgr, ref = make(orc, Hkv, D, 16, 77 + S)
+    step(mgr, ref, 0, Hq, Hkv, 31, D, 900, "prefill 31")   # next token opens page 2
+    before = layer_snapshot(mgr, 0)
+    buf = torch.zeros(Hq * S * D + 8, dtype=torch.bfloat16, device="cuda")
+    q_mis = buf[1:1 + Hq * S * D].view(1, Hq, S, D)          # 2-byte offset: not 16-byte aligned
+    q = paged.to_device_bf16(synth.normal_bf16(5, (1, Hq, S, D)))
+    kv = paged.to_device_bf16(synth.normal_bf16(6, (1, Hkv, S, D)))
+    out = torch.zeros((1, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    for label, args in (("misaligned q", (q_mis, kv, kv, out, Hq // Hkv, 0.1)),
+                        ("NaN scale", (q, kv, kv, out, Hq // Hkv, float("nan"))),
+                        ("infinite scale", (q, kv, kv, out, Hq // Hkv, float("inf")))):
+        with pytest.raises(GenllmError) as e:
+            paged.paged_attention(mgr, 0, *args)
+        assert e.value.code == ERR_INVALID, label
+        torch.cuda.synchronize()
+        assert layer_snapshot(mgr, 0) == before, f"{label} changed the layer"
+    step(mgr, ref, 0, Hq, Hkv, S, D, 901, "valid call after the errors")
+    assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0))
+    assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1))
+    mgr.close()
+
+
+def test_reserve_fits_exact_scheduler_sizing(orc):
+    """The kv_cache pool sized exactly as the reference scheduler does
+    (2 * max_blocks * block_bytes per layer, scheduler.cpp:62-79, 371) holds
+    every layer's pools: the device page tables and the decode workspace live
+    outside it.  One byte less and the last reserve_layer fails."""
+    from genllm_amd._lib import ERR_NO_MEMORY
+    Hq, Hkv, D, L, max_blocks = 32, 8, 128, 3, 40
+    exact = L * 2 * max_blocks * 16 * Hkv * D * 2
+    mgr = paged.PagedAttentionManager(exact)
+    for l in range(L):
+        mgr.init_layer(l, Hkv, D)
+        mgr.reserve_layer(l, max_blocks)
+    # the last layer's pools work: prefill chunks, then decode steps crossing a page
+    ref = orc.Manager(with_pool=True)
+    ref.init_layer(L - 1, Hkv, D)
+    ref.reserve_layer(L - 1, max_blocks)
+    for i, S in enumerate((17, 14, 1, 1)):
+        step(mgr, ref, L - 1, Hq, Hkv, S, D, 40 + i, f"exact-size step {i} S={S}")
+    mgr.close()
+    short = paged.PagedAttentionManager(exact - 1)
+    for l in range(L - 1):
+        short.init_layer(l, Hkv, D)
+        short.reserve_layer(l, max_blocks)
+    short.init_layer(L - 1, Hkv, D)
+    with pytest.raises(GenllmError) as e:
+        short.reserve_layer(L - 1, max_blocks)
+    assert e.value.code == ERR_NO_MEMORY
+    short.close()
