@@ -553,8 +553,8 @@ def measure_counters():
         t1 = max(v[-1][1] for v in timed.values())
         res["kernel_trace"] = {"mean_us": per_kernel, "sum_us": round(sum(per_kernel.values()), 3),
                                "timeline_us_per_decode": round((t1 - t0) / 1e3 / n, 3), "decodes": n,
-                               "note": "durations under rocprofv3 --kernel-trace; consecutive dispatches overlap "
-                                       "in their traced intervals, so sum_us exceeds the timeline per decode"}
+                               "note": "durations under rocprofv3 --kernel-trace, which itself adds about "
+                                       "0.6 us per dispatch against the event-timed avg_launch_us"}
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     res["bytes"] = res["FETCH_SIZE"]["bytes"] + res["WRITE_SIZE"]["bytes"]

@@ -4,8 +4,9 @@
 // Reference: include/core/page_attention.h:9-90, src/core/page_attention.cpp:25-216,
 // src/core/pools.cpp:17-48 (bump allocator), src/backend/cpu/attention.cpp:123-216
 // and src/backend/cuda/attention.cu:491-580 (the op).  Differences, by design:
-//   * the device page table lives in HBM next to the pools and is updated
-//     incrementally (the CUDA op mallocs, copies and frees it on every call);
+//   * the device page table lives in HBM (allocated once, at reserve_layer)
+//     and is updated incrementally (the CUDA op mallocs, copies and frees it
+//     on every call);
 //   * the K/V append is one kernel (the CUDA path issues 2*S*Hkv memcpys);
 //   * a pool without free pages is an error that leaves the layer unchanged
 //     (the reference breaks out of the loop but still advances num_cached).
