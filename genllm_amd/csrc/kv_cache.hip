@@ -12,6 +12,7 @@
 //     (the reference breaks out of the loop but still advances num_cached).
 #include <algorithm>
 #include <climits>
+#include <cstdint>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -832,6 +833,72 @@ extern "C" int genllm_paged_prefill(const void* q, int64_t q_head_stride, int64_
                              v_ids, n_pages, n_cached, seq_len, n_q_heads, n_kv_heads, head_dim, scale, causal);
     if (int rc = check_attn_args(p, head_dim)) return rc;
     return launch_paged_prefill(p, head_dim, as_stream(stream));
+}
+
+// ------------------------------------------------ allocation-free decode
+// Device scratch of genllm_paged_decode_noalloc: the arrival counters and the
+// split partials that genllm_paged_decode takes from its caller's workspace.
+// One copy per GPU the library runs on, held until the process ends.  In host
+// code `scratch` is only a stand-in for the symbol: its device address on the
+// current device comes from hipGetSymbolAddress (scratch_on_device).
+static __device__ __align__(256) unsigned char scratch[GENLLM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};  // device address of `scratch`, per device
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+// The scratch of the current device: resolved once per device, with its
+// arrival counters cleared by a small kernel on `stream` (no memset, so the
+// call may be captured into a graph).
+int scratch_on_device(hipStream_t stream, void** out) {
+    int dev = 0;
+    GENLLM_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(GENLLM_ERR_UNSUPPORTED, "paged_decode_noalloc: device id >= 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        GENLLM_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) return fail(GENLLM_ERR_HIP, "paged_decode_noalloc: scratch has no device address");
+        hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, stream, static_cast<uint32_t*>(ptr),
+                           int(kDecodeCounterBytes / sizeof(uint32_t)));
+        GENLLM_LAUNCH_CHECK("zero_words_kernel");
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return GENLLM_OK;
+}
+
+}  // namespace
+
+extern "C" int genllm_paged_decode_noalloc(const void* q, int64_t q_head_stride, int64_t q_tok_stride, void* out,
+                                           int64_t o_head_stride, int64_t o_tok_stride, const void* k_pool,
+                                           const void* v_pool, const int32_t* k_ids, const int32_t* v_ids,
+                                           int32_t n_pages, int32_t n_cached, int32_t seq_len, int32_t n_q_heads,
+                                           int32_t n_kv_heads, int32_t head_dim, float scale, int32_t causal,
+                                           void* stream) {
+    AttnParams p = make_attn(q, q_head_stride, q_tok_stride, out, o_head_stride, o_tok_stride, k_pool, v_pool, k_ids,
+                             v_ids, n_pages, n_cached, seq_len, n_q_heads, n_kv_heads, head_dim, scale, causal);
+    if (int rc = check_attn_args(p, head_dim)) return rc;
+    if (p.G * p.S > 16)
+        return fail(GENLLM_ERR_INVALID, "paged_decode_noalloc: seq_len * groups must be <= 16");
+    void* ws = nullptr;
+    if (int rc = scratch_on_device(as_stream(stream), &ws)) return rc;
+    if (int rc = decode_plan(p, head_dim, SIZE_MAX, ws)) return rc;
+    const size_t need = p.n_splits > 1 ? kDecodeCounterBytes + size_t(p.Hkv) * p.n_splits * size_t(p.G * p.S) *
+                                                                 size_t(head_dim + 2) * sizeof(float)
+                                       : 0;
+    if (need > GENLLM_NOALLOC_SCRATCH_BYTES)
+        return fail(GENLLM_ERR_INVALID, "paged_decode_noalloc: this launch needs " + std::to_string(need) +
+                                            " bytes of scratch, more than its fixed " +
+                                            std::to_string(size_t(GENLLM_NOALLOC_SCRATCH_BYTES)) +
+                                            " (use genllm_paged_decode with a workspace)");
+    return launch_paged_decode(p, head_dim, as_stream(stream));
 }
 
 // Non-paged attention (FlashAttentionImpl, attention.cpp:39-121): the prefill

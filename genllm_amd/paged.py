@@ -279,6 +279,16 @@ def paged_decode(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: i
          _ptr(workspace), ws_bytes, _stream(stream))
 
 
+def paged_decode_noalloc(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: int, n_kv_heads: int,
+                         scale: float, causal: bool = True, q_layout: str = "head", stream=None):
+    """paged_decode without a workspace: the library's static per-GPU scratch
+    holds the split partials (genllm_paged_decode_noalloc)."""
+    Hq, S, D, qs, os_ = _attn_args(q, out, q_layout)
+    call("genllm_paged_decode_noalloc", _ptr(q), qs[0], qs[1], _ptr(out), os_[0], os_[1], _ptr(k_pool), _ptr(v_pool),
+         _ptr(k_ids), _ptr(v_ids), n_pages, n_cached, S, Hq, n_kv_heads, D, float(scale), int(causal),
+         _stream(stream))
+
+
 def paged_prefill(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: int, n_kv_heads: int,
                   scale: float, causal: bool = True, q_layout: str = "head", stream=None):
     Hq, S, D, qs, os_ = _attn_args(q, out, q_layout)
@@ -341,6 +351,6 @@ def to_host_bits(t: torch.Tensor) -> np.ndarray:
 
 __all__ = [
     "PagedAttentionManager", "paged_attention", "qk_norm_rope_append", "rms_norm", "apply_rope", "rope_cache",
-    "kv_scatter", "paged_decode", "paged_prefill", "flash_attention", "decode_workspace_bytes", "fill_normal_bf16",
+    "kv_scatter", "paged_decode", "paged_decode_noalloc", "paged_prefill", "flash_attention", "decode_workspace_bytes", "fill_normal_bf16",
     "selftest_mfma", "device_view", "to_device_bf16", "to_host_bits", "GenllmError", "PAGE", "DTYPE_BF16",
 ]

@@ -195,6 +195,25 @@ int genllm_paged_decode(const void *q, int64_t q_head_stride, int64_t q_tok_stri
                         int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
                         int32_t causal, void *workspace, size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference: genllm_paged_decode for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and kernels, no
+ * workspace: the split partials and arrival counters live in a static device
+ * scratch of GENLLM_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends.  The call allocates nothing; its first call on a device resolves that
+ * device's scratch and clears its counters with a small kernel on `stream`.
+ * A launch whose split plan needs more scratch (kv heads x splits x rows x
+ * (head_dim + 2) x 4 bytes + 1 KiB; the Qwen3-4B decode at 8K or 32K keys
+ * needs about 0.5 MiB) returns GENLLM_ERR_INVALID and launches nothing.
+ * Every call on a GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (different streams, threads) race; calls ordered on one stream do not. */
+#define GENLLM_NOALLOC_SCRATCH_BYTES (4u << 20)
+int genllm_paged_decode_noalloc(const void *q, int64_t q_head_stride, int64_t q_tok_stride, void *out,
+                                int64_t o_head_stride, int64_t o_tok_stride, const void *k_pool, const void *v_pool,
+                                const int32_t *k_ids, const int32_t *v_ids, int32_t n_pages, int32_t n_cached,
+                                int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                float scale, int32_t causal, void *stream);
+
 /* The same attention loop for long query chunks (prefill): bf16 MFMA
  * FlashAttention over page-gathered K/V tiles, causal with query s at
  * n_cached - seq_len + s. */
