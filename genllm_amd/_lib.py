@@ -83,6 +83,11 @@ SIGNATURES = {
     "genllm_kv_block_alloc": (_int, [_P, _i32, _i32, C.POINTER(_i32)]),
     "genllm_kv_block_free": (_int, [_P, _i32, _i32, _i32]),
     "genllm_paged_attention": (_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, _i32, _P]),
+    "genllm_kv_stage_decode": (_int, [_P, _i32, _i32, _P]),
+    "genllm_kv_sync_decode": (_int, [_P, _i32, _P, _P]),
+    "genllm_paged_attention_step": (_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, _i32,
+                                           _P]),
+    "genllm_apply_rope_step": (_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _P]),
     "genllm_qk_norm_rope_append": (_int, [_P, _i32, _i32, _P, _i64, _i64, _P, _i64, _i64, _P, _P, _i64, _i64,
                                           _i32, _P, _P, _i64, _i64, _f, _P, _P, _i32, _i64, _P]),
     "genllm_rms_norm": (_int, [_P, _P, _P, _i64, _i32, _f, _P]),

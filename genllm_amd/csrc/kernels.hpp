@@ -79,6 +79,14 @@ struct AttnParams {
     // launches); the last split workgroup of a head to arrive merges them.
     // nullptr = merge in a second kernel.
     int32_t* counters = nullptr;
+    // Device-position step (graph-capturable decode): control block
+    // {pos, limit, arrivals, error} (kStep* indices).  When set, the kernel
+    // reads the cache position from it -- n_cached = pos + S, new_from = pos,
+    // pages = ceil(n_cached / 16) -- instead of n_cached / new_from / n_pages,
+    // which then only size the plan (n_pages = the most pages a step may
+    // span).  A step past `limit` (or past n_pages) sets `error` and does
+    // nothing; otherwise the last workgroup to finish advances pos by S.
+    int32_t* step = nullptr;
     // fused append (decode of the op): tokens at positions >= new_from are read
     // from k_new / v_new ([Hkv][S][D], strides in elements) instead of the
     // pools and written into the pools by the wave that reads their page; page
@@ -99,6 +107,9 @@ struct AttnParams {
 // them at zero), then the per-split partials.
 constexpr size_t kDecodeCounterBytes = 1024;
 constexpr int kDecodeMaxKvHeads = int(kDecodeCounterBytes / sizeof(int32_t));
+// Device-position step control block (int32 indices); arrivals and error
+// must be zero before the first step.
+constexpr int kStepPos = 0, kStepLimit = 1, kStepArrivals = 2, kStepError = 3, kStepInts = 4;
 size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages);
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws);
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream);
@@ -106,7 +117,10 @@ int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream);
 
 int launch_rms_norm(uint16_t* out, const uint16_t* x, const float* w, int64_t rows, int hidden, float eps,
                     hipStream_t stream);
+// ctl != nullptr: start position from a device-position step control block
+// (start_pos ignored), checked against the table's max_seq rows.
 int launch_apply_rope(uint16_t* out, const uint16_t* x, const float* cos_tab, const float* sin_tab, int n_heads,
-                      int seq_len, int head_dim, int rope_dim, int64_t start_pos, hipStream_t stream);
+                      int seq_len, int head_dim, int rope_dim, int64_t start_pos, hipStream_t stream,
+                      int32_t* ctl = nullptr, int64_t max_seq = 0);
 
 }  // namespace genllm

@@ -111,6 +111,18 @@ struct LayerState {
     int32_t* h_ids = nullptr;
     int32_t max_blocks = 0;
     size_t block_bytes = 0;
+    // Device-position decode (graph-capturable steps): the control block
+    // {pos, limit, arrivals, error} follows the device page table.  Between
+    // genllm_kv_stage_decode and genllm_kv_sync_decode the device owns the
+    // position; num_cached and the tables then describe the end of the staged
+    // window, and stage_k / stage_v list the blocks staging handed out (in
+    // allocation order, with their free-list origin) so that the unused ones
+    // can be given back exactly.
+    int32_t* d_step = nullptr;
+    bool staged = false;
+    int32_t stage_num_cached = 0;
+    size_t stage_table_size = 0;
+    std::vector<std::pair<int32_t, bool>> stage_k, stage_v;
 };
 
 }  // namespace genllm
@@ -256,6 +268,28 @@ LayerState* active_layer(genllm_kv* kv, int32_t layer) {
     return &it->second;
 }
 
+// Host-driven changes of a layer whose position the device owns would break
+// the exact rewind of genllm_kv_sync_decode: they are refused until then.
+int refuse_staged(const LayerState& s, const char* what) {
+    return s.staged ? fail(GENLLM_ERR_INVALID, std::string(what) +
+                                                   ": the layer is staged for device-position decode "
+                                                   "(call genllm_kv_sync_decode first)")
+                    : GENLLM_OK;
+}
+
+// Writes the device-position control block: limit always; when `enter`,
+// also the position, with the arrival counter and the error flag cleared.
+// A kernel, not a memset or copy, so it needs no host buffer to outlive it.
+__global__ void set_step_kernel(int32_t* ctl, int32_t pos, int32_t limit, int32_t enter) {
+    if (threadIdx.x != 0) return;
+    if (enter) {
+        ctl[kStepPos] = pos;
+        ctl[kStepArrivals] = 0;
+        ctl[kStepError] = 0;
+    }
+    ctl[kStepLimit] = limit;
+}
+
 // Split-K workspace of the manager, grown at set-up only (reserve_layer) to
 // the largest decode plan any reserved layer can make: 16 rows per kv head
 // (the decode kernel's limit) and as many splits as the layer's max_blocks
@@ -377,6 +411,7 @@ extern "C" int genllm_kv_init_layer(genllm_kv* kv, int32_t layer, int32_t n_kv_h
     s.dtype = dtype;
     s.active = true;
     s.num_cached = 0;
+    s.staged = false;
     return GENLLM_OK;
 }
 
@@ -401,7 +436,9 @@ extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max
     GENLLM_HIP_TRY(hipSetDevice(kv->device));
     void* table = nullptr;
     void* staging = nullptr;
-    hipError_t e = hipMalloc(&table, size_t(max_blocks) * 2 * sizeof(int32_t));
+    const size_t table_bytes = (size_t(max_blocks) * 2 + kStepInts) * sizeof(int32_t);
+    hipError_t e = hipMalloc(&table, table_bytes);
+    if (e == hipSuccess) e = hipMemset(table, 0, table_bytes);
     if (e == hipSuccess) e = hipHostMalloc(&staging, size_t(max_blocks) * 2 * sizeof(int32_t), hipHostMallocDefault);
     if (e != hipSuccess) {
         if (table) (void)hipFree(table);
@@ -419,6 +456,8 @@ extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max
     s.v_base = static_cast<uint16_t*>(vp);
     s.d_k_ids = static_cast<int32_t*>(table);
     s.d_v_ids = static_cast<int32_t*>(table) + max_blocks;
+    s.d_step = static_cast<int32_t*>(table) + 2 * size_t(max_blocks);
+    s.staged = false;
     s.block_bytes = bb;
     s.max_blocks = max_blocks;
     s.k_pool = BlockPool{};
@@ -437,6 +476,7 @@ extern "C" int genllm_kv_is_active(genllm_kv* kv, int32_t layer, int32_t* active
 extern "C" int genllm_kv_append_pages(genllm_kv* kv, int32_t layer, int32_t count, void* stream) {
     if (!kv) return fail(GENLLM_ERR_INVALID, "append_pages: null kv");
     LayerState& s = kv->layers[layer];
+    if (int rc = refuse_staged(s, "append_pages")) return rc;
     return append_pages<TableUpdate>(kv, s, count, as_stream(stream), nullptr);
 }
 
@@ -449,6 +489,9 @@ extern "C" int genllm_kv_reset(genllm_kv* kv) {
         s.v_ids.clear();
         s.k_pool.reset();
         s.v_pool.reset();
+        s.staged = false;  // the device position is re-uploaded by the next staging
+        s.stage_k.clear();
+        s.stage_v.clear();
     }
     return GENLLM_OK;
 }
@@ -498,6 +541,7 @@ extern "C" int genllm_kv_set_page_table(genllm_kv* kv, int32_t layer, const int3
     if (!kv || (n > 0 && (!k_ids || !v_ids))) return fail(GENLLM_ERR_INVALID, "set_page_table: null pointer");
     LayerState* s = active_layer(kv, layer);
     if (!s) return fail(GENLLM_ERR_INVALID, "set_page_table: layer not active");
+    if (int rc = refuse_staged(*s, "set_page_table")) return rc;
     if (n < 0 || num_cached < 0 || (s->max_blocks > 0 && n > s->max_blocks) || int64_t(num_cached) > int64_t(n) * kPage)
         return fail(GENLLM_ERR_INVALID, "set_page_table: bad length or num_cached");
     for (int32_t i = 0; i < n; ++i)
@@ -520,6 +564,7 @@ extern "C" int genllm_kv_set_page_table(genllm_kv* kv, int32_t layer, const int3
 extern "C" int genllm_kv_block_alloc(genllm_kv* kv, int32_t layer, int32_t which, int32_t* id) {
     if (!kv || !id) return fail(GENLLM_ERR_INVALID, "block_alloc: null pointer");
     LayerState& s = kv->layers[layer];
+    if (int rc = refuse_staged(s, "block_alloc")) return rc;
     *id = (which ? s.v_pool : s.k_pool).alloc();
     return GENLLM_OK;
 }
@@ -527,50 +572,41 @@ extern "C" int genllm_kv_block_alloc(genllm_kv* kv, int32_t layer, int32_t which
 extern "C" int genllm_kv_block_free(genllm_kv* kv, int32_t layer, int32_t which, int32_t id) {
     if (!kv) return fail(GENLLM_ERR_INVALID, "block_free: null kv");
     LayerState& s = kv->layers[layer];
+    if (int rc = refuse_staged(s, "block_free")) return rc;
     (which ? s.v_pool : s.k_pool).free(id);
     return GENLLM_OK;
 }
 
 // ------------------------------------------------------------------ the op
-extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* q, const void* k, const void* v,
-                                      void* out, int32_t batch, int32_t n_q_heads, int32_t seq_len,
-                                      int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups, float scale,
-                                      int32_t causal, void* stream) {
-    if (!kv) return fail(GENLLM_ERR_INVALID, "paged_attention: null kv");
-    LayerState* s = active_layer(kv, layer);
-    if (!s) return GENLLM_OK;  // attention.cpp:127: inactive layer, nothing written
+namespace {
+
+// Argument checks of the op and its attention parameters for a layer holding
+// n_after tokens once this call's seq_len tokens are appended.
+int op_params(const LayerState& s, const void* q, const void* k, const void* v, void* out, int32_t batch,
+              int32_t n_q_heads, int32_t seq_len, int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups,
+              float scale, int32_t causal, int32_t n_after, AttnParams& p) {
     if (head_dim != 128 && head_dim != 256)
         return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention requires head_dim 128 or 256");
     if (batch != 1) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention: batch must be 1");
-    if (s->dtype != GENLLM_DTYPE_BF16 || s->head_dim != head_dim || s->n_kv_heads != n_kv_heads)
+    if (s.dtype != GENLLM_DTYPE_BF16 || s.head_dim != head_dim || s.n_kv_heads != n_kv_heads)
         return fail(GENLLM_ERR_INVALID, "paged_attention: tensor shape/dtype differs from the layer's pools");
     if (n_kv_groups <= 0 || n_q_heads != n_kv_heads * n_kv_groups)
         return fail(GENLLM_ERR_INVALID, "paged_attention: n_q_heads must equal n_kv_heads * n_kv_groups");
     if (!q || !k || !v || !out) return fail(GENLLM_ERR_INVALID, "paged_attention: null tensor");
-    if (!s->k_base) return fail(GENLLM_ERR_INVALID, "paged_attention: layer has no reserved pools");
-    if (seq_len <= 0) return GENLLM_OK;
+    if (!s.k_base) return fail(GENLLM_ERR_INVALID, "paged_attention: layer has no reserved pools");
     if (!aligned(k, 16) || !aligned(v, 16))
         return fail(GENLLM_ERR_INVALID, "paged_attention: k/v must be 16-byte aligned");
-    hipStream_t st = as_stream(stream);
-    const int32_t pos0 = s->num_cached;
-    if (int64_t(pos0) + seq_len > int64_t(INT32_MAX) - kPage)
-        return fail(GENLLM_ERR_INVALID, "paged_attention: position overflow");
-    const int32_t n_after = pos0 + seq_len;
-    const bool fuse = int64_t(n_kv_groups) * seq_len <= 16;
-
-    // 0. attention arguments and split plan for the state after the append,
-    // checked before anything changes: an error leaves the layer as it was
-    AttnParams p;
+    p = AttnParams{};
     p.q = static_cast<const uint16_t*>(q);
     p.q_head_stride = int64_t(seq_len) * head_dim;
     p.q_tok_stride = head_dim;
     p.out = static_cast<uint16_t*>(out);
     p.o_head_stride = int64_t(seq_len) * head_dim;
     p.o_tok_stride = head_dim;
-    p.k_pool = s->k_base;
-    p.v_pool = s->v_base;
-    p.k_ids = s->d_k_ids;
-    p.v_ids = s->d_v_ids;
+    p.k_pool = s.k_base;
+    p.v_pool = s.v_base;
+    p.k_ids = s.d_k_ids;
+    p.v_ids = s.d_v_ids;
     p.n_cached = n_after;
     p.n_pages = (n_after + kPage - 1) / kPage;
     p.S = seq_len;
@@ -581,6 +617,52 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     p.causal = causal != 0;
     p.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
     p.kv_row = int64_t(n_kv_heads) * head_dim;
+    return GENLLM_OK;
+}
+
+// The decode kernel's fused append: new rows (head-major [Hkv][S][D]) come
+// from k / v and are written to the pools by the waves that read their pages.
+void fuse_append(AttnParams& p, const LayerState& s, const void* k, const void* v, int32_t seq_len,
+                 int32_t head_dim, int32_t new_from) {
+    p.k_new = static_cast<const uint16_t*>(k);
+    p.v_new = static_cast<const uint16_t*>(v);
+    p.new_head_stride = int64_t(seq_len) * head_dim;
+    p.new_tok_stride = head_dim;
+    p.new_from = new_from;
+    p.k_pool_w = s.k_base;
+    p.v_pool_w = s.v_base;
+    p.k_ids_w = s.d_k_ids;
+    p.v_ids_w = s.d_v_ids;
+}
+
+}  // namespace
+
+extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* q, const void* k, const void* v,
+                                      void* out, int32_t batch, int32_t n_q_heads, int32_t seq_len,
+                                      int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups, float scale,
+                                      int32_t causal, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "paged_attention: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return GENLLM_OK;  // attention.cpp:127: inactive layer, nothing written
+    if (int rc = refuse_staged(*s, "paged_attention")) return rc;
+    if (seq_len <= 0) {
+        AttnParams unused;
+        return op_params(*s, q, k, v, out, batch, n_q_heads, 1, head_dim, n_kv_heads, n_kv_groups, scale, causal,
+                         1, unused);
+    }
+    hipStream_t st = as_stream(stream);
+    const int32_t pos0 = s->num_cached;
+    if (int64_t(pos0) + seq_len > int64_t(INT32_MAX) - kPage)
+        return fail(GENLLM_ERR_INVALID, "paged_attention: position overflow");
+    const int32_t n_after = pos0 + seq_len;
+    const bool fuse = int64_t(n_kv_groups) * seq_len <= 16;
+
+    // 0. attention arguments and split plan for the state after the append,
+    // checked before anything changes: an error leaves the layer as it was
+    AttnParams p;
+    if (int rc = op_params(*s, q, k, v, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads, n_kv_groups, scale,
+                           causal, n_after, p))
+        return rc;
     if (int rc = prepare_attention(p, head_dim, kv)) return rc;
 
     // 1. append (append_kv_from_tensor, attention.cpp:146): head-major [Hkv][S][D].
@@ -613,15 +695,7 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
 
     // 2. attend over all cached tokens
     if (fuse) {
-        p.k_new = ap.k;
-        p.v_new = ap.v;
-        p.new_head_stride = ap.k_head_stride;
-        p.new_tok_stride = ap.k_tok_stride;
-        p.new_from = pos0;
-        p.k_pool_w = s->k_base;
-        p.v_pool_w = s->v_base;
-        p.k_ids_w = s->d_k_ids;
-        p.v_ids_w = s->d_v_ids;
+        fuse_append(p, *s, k, v, seq_len, head_dim, pos0);
         // seq_len <= 16 opens at most 2 pages, which fit the launch arguments
         // (append_pages put them in ap.upd, as it holds up to 256)
         static_assert(sizeof(p.upd.k) / sizeof(int32_t) >= 2, "decode step opens up to 2 pages");
@@ -639,6 +713,117 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     return GENLLM_OK;
 }
 
+// ------------------------------------------------ device-position decode
+// The reference's decode loop (src/core/executor.cpp:227-236) advances the
+// position every step, and each step's append opens a page whenever the
+// position crosses a multiple of 16 (append_kv_pages, page_attention.cpp:
+// 141-162).  For a step captured once into a HIP graph and replayed, both
+// move to the device: staging opens, ahead of time and in the order the steps
+// would, the pages of a window of future tokens; the step reads the position
+// from the layer's control block and its last workgroup advances it; sync
+// reads it back and returns the staged pages no step reached.
+
+extern "C" int genllm_kv_stage_decode(genllm_kv* kv, int32_t layer, int32_t n_tokens, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "stage_decode: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return fail(GENLLM_ERR_INVALID, "stage_decode: layer not active");
+    if (!s->d_step) return fail(GENLLM_ERR_INVALID, "stage_decode: layer has no reserved pools");
+    if (n_tokens < 0) return fail(GENLLM_ERR_INVALID, "stage_decode: n_tokens must be >= 0");
+    hipStream_t st = as_stream(stream);
+    const bool enter = !s->staged;
+    const int32_t pos = s->num_cached;
+    const size_t table0 = s->k_ids.size();
+    AppendUndo& undo = t_undo;
+    if (int rc = append_pages(kv, *s, n_tokens, st, static_cast<TableUpdate*>(nullptr), &undo)) return rc;
+    GENLLM_HIP_TRY(hipSetDevice(kv->device));
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(64), 0, st, s->d_step, pos, s->num_cached, int32_t(enter));
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) {
+        undo_append(*s, undo);
+        return hip_fail(e, "stage_decode: set_step_kernel");
+    }
+    if (enter) {
+        s->staged = true;
+        s->stage_num_cached = pos;
+        s->stage_table_size = table0;
+        s->stage_k.clear();
+        s->stage_v.clear();
+    }
+    s->stage_k.insert(s->stage_k.end(), undo.k.begin(), undo.k.end());
+    s->stage_v.insert(s->stage_v.end(), undo.v.begin(), undo.v.end());
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_kv_sync_decode(genllm_kv* kv, int32_t layer, void* stream, int32_t* num_cached) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "sync_decode: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return fail(GENLLM_ERR_INVALID, "sync_decode: layer not active");
+    if (!s->staged) {
+        if (num_cached) *num_cached = s->num_cached;
+        return GENLLM_OK;
+    }
+    hipStream_t st = as_stream(stream);
+    GENLLM_HIP_TRY(hipSetDevice(kv->device));
+    int32_t ctl[kStepInts] = {};
+    GENLLM_HIP_TRY(hipMemcpyAsync(ctl, s->d_step, sizeof ctl, hipMemcpyDeviceToHost, st));
+    GENLLM_HIP_TRY(hipStreamSynchronize(st));
+    const int32_t pos = ctl[kStepPos];
+    if (pos < s->stage_num_cached || pos > s->num_cached)
+        return fail(GENLLM_ERR_INVALID, "sync_decode: device position " + std::to_string(pos) +
+                                             " outside the staged window [" + std::to_string(s->stage_num_cached) +
+                                             ", " + std::to_string(s->num_cached) + "]");
+    // Staging handed out one K and one V block per page the window opens, in
+    // position order.  The steps that ran used the first `used`; the rest go
+    // back in reverse order, which restores the pools exactly, and the table
+    // keeps the entries the reference's appends up to `pos` would have pushed.
+    const int64_t used = pages_opened(s->stage_num_cached, pos - s->stage_num_cached);
+    for (size_t i = s->stage_k.size(); i-- > size_t(used);) {
+        s->k_pool.unalloc(s->stage_k[i].first, s->stage_k[i].second);
+        s->v_pool.unalloc(s->stage_v[i].first, s->stage_v[i].second);
+    }
+    const size_t first = size_t((int64_t(s->stage_num_cached) + kPage - 1) / kPage);
+    const size_t keep = std::max(s->stage_table_size, first + size_t(used));
+    if (keep < s->k_ids.size()) {
+        s->k_ids.resize(keep);
+        s->v_ids.resize(keep);
+    }
+    s->num_cached = pos;
+    s->staged = false;
+    s->stage_k.clear();
+    s->stage_v.clear();
+    if (num_cached) *num_cached = pos;
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(64), 0, st, s->d_step, pos, pos, 1);
+    GENLLM_LAUNCH_CHECK("set_step_kernel");
+    if (ctl[kStepError])
+        return fail(GENLLM_ERR_POOL_FULL, "decode step: a step at position " + std::to_string(pos) +
+                                              " would pass the staged window; it and the steps after it did "
+                                              "nothing (the layer now holds " + std::to_string(pos) + " tokens)");
+    return GENLLM_OK;
+}
+
+extern "C" int genllm_paged_attention_step(genllm_kv* kv, int32_t layer, const void* q, const void* k,
+                                           const void* v, void* out, int32_t batch, int32_t n_q_heads,
+                                           int32_t seq_len, int32_t head_dim, int32_t n_kv_heads,
+                                           int32_t n_kv_groups, float scale, int32_t causal, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "paged_attention_step: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return GENLLM_OK;  // attention.cpp:127
+    if (!s->staged) return fail(GENLLM_ERR_INVALID, "paged_attention_step: layer not staged (genllm_kv_stage_decode)");
+    if (seq_len <= 0 || int64_t(n_kv_groups) * seq_len > 16)
+        return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention_step: seq_len * n_kv_groups must be in [1, 16]");
+    // Planned for the end of the staged window: the grid covers every page a
+    // step inside it can reach; splits past a step's last page are empty.
+    const int32_t window_end = std::max(s->num_cached, seq_len);
+    AttnParams p;
+    if (int rc = op_params(*s, q, k, v, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads, n_kv_groups, scale,
+                           causal, window_end, p))
+        return rc;
+    if (int rc = prepare_attention(p, head_dim, kv)) return rc;
+    fuse_append(p, *s, k, v, seq_len, head_dim, 0);
+    p.step = s->d_step;
+    return launch_attention(p, head_dim, as_stream(stream));
+}
+
+
 extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t seq_len, const void* k,
                                           int64_t k_tok_stride, int64_t k_head_stride, const void* v,
                                           int64_t v_tok_stride, int64_t v_head_stride, const float* gamma_k,
@@ -650,6 +835,7 @@ extern "C" int genllm_qk_norm_rope_append(genllm_kv* kv, int32_t layer, int32_t 
     if (!kv) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: null kv");
     LayerState* s = active_layer(kv, layer);
     if (!s) return GENLLM_OK;
+    if (int rc = refuse_staged(*s, "qk_norm_rope_append")) return rc;
     if (!s->k_base) return fail(GENLLM_ERR_INVALID, "qk_norm_rope_append: layer has no reserved pools");
     const int D = s->head_dim;
     if (D != 64 && D != 128 && D != 256) return fail(GENLLM_ERR_UNSUPPORTED, "qk_norm_rope_append: head_dim");
@@ -727,6 +913,21 @@ extern "C" int genllm_apply_rope(void* out, const void* x, const float* cos_tab,
         return fail(GENLLM_ERR_INVALID, "apply_rope: bad arguments");
     return launch_apply_rope(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(x), cos_tab, sin_tab,
                              n_heads, seq_len, head_dim, rope_dim, start_pos, as_stream(stream));
+}
+
+// ApplyRopeImpl for a device-position decode step: as genllm_apply_rope with
+// start_pos = the staged layer's device position (read when the kernel runs).
+extern "C" int genllm_apply_rope_step(genllm_kv* kv, int32_t layer, void* out, const void* x, const float* cos_tab,
+                                      const float* sin_tab, int32_t n_heads, int32_t seq_len, int32_t head_dim,
+                                      int32_t rope_dim, int32_t max_seq, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "apply_rope_step: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s || !s->staged) return fail(GENLLM_ERR_INVALID, "apply_rope_step: layer not staged (genllm_kv_stage_decode)");
+    if (!out || !x || !cos_tab || !sin_tab || head_dim <= 0 || head_dim % 2 || rope_dim <= 0 || rope_dim % 2 ||
+        rope_dim > head_dim || max_seq <= 0)
+        return fail(GENLLM_ERR_INVALID, "apply_rope_step: bad arguments");
+    return launch_apply_rope(static_cast<uint16_t*>(out), static_cast<const uint16_t*>(x), cos_tab, sin_tab,
+                             n_heads, seq_len, head_dim, rope_dim, 0, as_stream(stream), s->d_step, max_seq);
 }
 
 extern "C" int genllm_rope_cache(float* dst, float theta, int32_t head_dim, int32_t max_seq, int32_t is_cos) {

@@ -62,10 +62,26 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t* out, const uint
 // the pair (i, i + rope_dim/2) with table entry [pos][i] (rows of rope_dim
 // floats); slot i >= rope_dim/2 copies the two elements rope_dim + 2(i -
 // rope_dim/2) + {0, 1} unchanged.  rope_dim == head_dim is the reference op.
+// With `ctl` (a device-position decode step) the start position is the
+// control block's pos; a step whose rows would pass the table's max_seq rows
+// raises the block's error flag and writes nothing, as does any step after a
+// refused one (the flag stays set until the host syncs the layer).
+template <bool kDevPos>
 __global__ __launch_bounds__(256) void apply_rope_kernel(uint16_t* out, const uint16_t* x, const float* cos_tab,
                                                          const float* sin_tab, int64_t rows, int seq_len,
-                                                         int head_dim, int rope_dim, int64_t start_pos) {
+                                                         int head_dim, int rope_dim, int64_t start_pos,
+                                                         int32_t* ctl, int64_t max_seq) {
     const int half = head_dim / 2, rhalf = rope_dim / 2;
+    if constexpr (kDevPos) {
+        start_pos = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(ctl + kStepPos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (__hip_atomic_load(ctl + kStepError, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+        if (start_pos < 0 || start_pos + seq_len > max_seq) {
+            if (blockIdx.x == 0 && threadIdx.x == 0)
+                __hip_atomic_store(ctl + kStepError, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= rows * half) return;
     const int64_t row = idx / half;
@@ -96,13 +112,18 @@ int launch_rms_norm(uint16_t* out, const uint16_t* x, const float* w, int64_t ro
 }
 
 int launch_apply_rope(uint16_t* out, const uint16_t* x, const float* cos_tab, const float* sin_tab, int n_heads,
-                      int seq_len, int head_dim, int rope_dim, int64_t start_pos, hipStream_t stream) {
+                      int seq_len, int head_dim, int rope_dim, int64_t start_pos, hipStream_t stream, int32_t* ctl,
+                      int64_t max_seq) {
     const int64_t rows = int64_t(n_heads) * seq_len;
     const int64_t n = rows * (head_dim / 2);
     if (n <= 0) return GENLLM_OK;
     const int64_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(apply_rope_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream, out, x, cos_tab, sin_tab,
-                       rows, seq_len, head_dim, rope_dim, start_pos);
+    if (ctl)
+        hipLaunchKernelGGL(apply_rope_kernel<true>, dim3(unsigned(blocks)), dim3(256), 0, stream, out, x, cos_tab,
+                           sin_tab, rows, seq_len, head_dim, rope_dim, int64_t(0), ctl, max_seq);
+    else
+        hipLaunchKernelGGL(apply_rope_kernel<false>, dim3(unsigned(blocks)), dim3(256), 0, stream, out, x, cos_tab,
+                           sin_tab, rows, seq_len, head_dim, rope_dim, start_pos, ctl, max_seq);
     GENLLM_LAUNCH_CHECK("apply_rope_kernel");
     return GENLLM_OK;
 }

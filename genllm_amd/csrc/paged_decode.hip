@@ -201,7 +201,14 @@ struct PageRegs {
     uint4 v[4][D / 128];   // V rows of tokens 4g..4g+3, dims 8 n16 + 128 hh
 };
 
-template <int D, int W>
+// Reads a word of the step control block at the device's coherence point
+// (written by the previous step's last workgroup on another XCD).
+__device__ __forceinline__ int step_load(const int32_t* at) {
+    return __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(const_cast<int32_t*>(at), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+template <int D, int W, bool kStep>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     static_assert(D == 128 || D == 256, "decode kernel: head_dim 128 or 256");
     constexpr int KS = D / 32;   // S^T k-steps
@@ -218,10 +225,28 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     const int h = blockIdx.x, sp = blockIdx.y;
     const int rows_total = p.G * p.S;  // <= 16
 
+    // Cache position: from the launch arguments, or (device-position step)
+    // from the control block, where a step that would pass the staged limit
+    // or the pages the grid was planned for only raises the error flag.
+    int n_cached = p.n_cached, n_pages = p.n_pages, new_from = p.new_from, step_pos = 0;
+    if constexpr (kStep) {
+        step_pos = step_load(p.step + kStepPos);
+        const int limit = step_load(p.step + kStepLimit);
+        if (step_load(p.step + kStepError)) return;  // an earlier kernel of this or a previous step was refused
+        if (step_pos < 0 || step_pos > limit - p.S || (step_pos + p.S + kPage - 1) / kPage > p.n_pages) {
+            if (threadIdx.x == 0)
+                __hip_atomic_store(p.step + kStepError, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        n_cached = step_pos + p.S;
+        n_pages = (n_cached + kPage - 1) / kPage;
+        new_from = step_pos;
+    }
+
     // this lane's row (MFMA column): q head h*G + r%G, query r/G
     const int r = n16;
     const bool row_ok = r < rows_total;
-    const int qabs = p.causal ? p.n_cached - p.S + r / p.G : p.n_cached - 1;
+    const int qabs = p.causal ? n_cached - p.S + r / p.G : n_cached - 1;
     bf16x8_t qb[KS];
     {
         const uint16_t* qrow = p.q + int64_t(h * p.G + r % p.G) * p.q_head_stride + int64_t(r / p.G) * p.q_tok_stride;
@@ -234,7 +259,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     }
 
     const int begin = sp * p.pages_per_split;
-    const int end = min(begin + p.pages_per_split, p.n_pages);
+    const int end = min(begin + p.pages_per_split, n_pages);
     const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;
     // fused append: page ids opened by this call come from the launch arguments
     if (sp == 0 && h == 0 && threadIdx.x < p.upd.count) {
@@ -265,7 +290,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     // Pages from special_from on hold the end of the cache: keys a query may
     // not see (causal), slots past n_cached and, in the fused op, the appended
     // tokens.  Only they take the per-token conditions below.
-    const int lo_tok = min(p.causal ? p.n_cached - p.S + 1 : p.n_cached, p.new_from);
+    const int lo_tok = min(p.causal ? n_cached - p.S + 1 : n_cached, new_from);
     const int special_from = lo_tok / kPage;
     auto page_of = [&](int j) { return begin + wv + W * j; };
 
@@ -297,8 +322,8 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         const uint16_t* kr = kb + kcol;
         if (fused) {
             const int tk = pg * kPage + n16;
-            if (tk >= p.new_from && tk < p.n_cached)
-                kr = p.k_new + h * p.new_head_stride + int64_t(tk - p.new_from) * p.new_tok_stride + 8 * g;
+            if (tk >= new_from && tk < n_cached)
+                kr = p.k_new + h * p.new_head_stride + int64_t(tk - new_from) * p.new_tok_stride + 8 * g;
         }
 #pragma unroll
         for (int c = 0; c < KS; ++c) pr.k[c] = *reinterpret_cast<const uint4*>(kr + 32 * c);
@@ -307,8 +332,8 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
             const uint16_t* src = vb + i * p.kv_row + vcol;
             if (fused) {
                 const int tv = pg * kPage + 4 * g + i;
-                if (tv >= p.new_from && tv < p.n_cached)
-                    src = p.v_new + h * p.new_head_stride + int64_t(tv - p.new_from) * p.new_tok_stride + 8 * n16;
+                if (tv >= new_from && tv < n_cached)
+                    src = p.v_new + h * p.new_head_stride + int64_t(tv - new_from) * p.new_tok_stride + 8 * n16;
             }
 #pragma unroll
             for (int hh = 0; hh < VH; ++hh) pr.v[i][hh] = *reinterpret_cast<const uint4*>(src + 128 * hh);
@@ -317,18 +342,18 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     // ... and write the appended rows into their page slots (bit-exact copies)
     auto store_new = [&](int j, const PageRegs<D>& pr) {
         const int pg = page_of(j);
-        if (pg * kPage + kPage <= p.new_from) return;  // wave-uniform: no new token in this page
+        if (pg * kPage + kPage <= new_from) return;  // wave-uniform: no new token in this page
         uint16_t* kb = p.k_pool_w + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
         uint16_t* vb = p.v_pool_w + int64_t(__builtin_amdgcn_readlane(my_vid, j)) * p.page_elems;
         const int tk = pg * kPage + n16;
-        if (tk >= p.new_from && tk < p.n_cached) {
+        if (tk >= new_from && tk < n_cached) {
 #pragma unroll
             for (int c = 0; c < KS; ++c) *reinterpret_cast<uint4*>(kb + kcol + 32 * c) = pr.k[c];
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tv = pg * kPage + 4 * g + i;
-            if (tv >= p.new_from && tv < p.n_cached)
+            if (tv >= new_from && tv < n_cached)
 #pragma unroll
                 for (int hh = 0; hh < VH; ++hh) *reinterpret_cast<uint4*>(vb + i * p.kv_row + vcol + 128 * hh) = pr.v[i][hh];
         }
@@ -348,7 +373,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 v[i] = pr.v[i][hh];
-                if (special && tok0 + i >= p.n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots
+                if (special && tok0 + i >= n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots
             }
             const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
                                       {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
@@ -372,7 +397,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = tok0 + i;
-            x[i] = (!special || (t < p.n_cached && t <= qabs)) ? s[i] * p.scale_log2 : -INFINITY;
+            x[i] = (!special || (t < n_cached && t <= qabs)) ? s[i] * p.scale_log2 : -INFINITY;
             lmx = fmaxf(lmx, x[i]);
         }
         // Lazy rescale: the row's reference max m_run only moves (and o, l are
@@ -501,6 +526,20 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
             if (lane == 0) store(make_float2(M, L), ml_off);
         }
     }
+    if constexpr (kStep) {
+        // Every workgroup read the position before it counts here, so the
+        // last to arrive may advance it (and re-arm the counter) for the next
+        // step.  The kernel boundary publishes both to the next launch.
+        if (threadIdx.x == 0) {
+            const int total = int(gridDim.x * gridDim.y);
+            const int old =
+                __hip_atomic_fetch_add(p.step + kStepArrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == total - 1) {
+                __hip_atomic_store(p.step + kStepArrivals, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.step + kStepPos, step_pos + p.S, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
     if (p.counters && p.n_splits > 1) merge_last_arrival<D, W>(p, h, lds_m, lds_l, lds_o);
 }
 
@@ -523,6 +562,8 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
     __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int h = blockIdx.x, ri = blockIdx.y;
+    // device-position step refused by the split kernel: no partials to merge
+    if (p.step && step_load(p.step + kStepError)) return;
     const int rows = p.G * p.S;
     const int ns = p.n_splits;  // <= kMaxSplits
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
@@ -660,17 +701,26 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
     return GENLLM_OK;
 }
 
-template <int D>
-int launch_decode_d(const AttnParams& p, hipStream_t stream) {
+template <int D, bool kStep>
+void launch_split(const AttnParams& p, hipStream_t stream) {
     bool wide = false;
     if constexpr (D == 128) {
         wide = p.pages_per_split <= kWideMaxPps;
         if (wide)
-            hipLaunchKernelGGL((paged_decode_kernel<D, kWideWaves>), dim3(p.Hkv, p.n_splits), dim3(kWideWaves * 64), 0,
-                               stream, p);
+            hipLaunchKernelGGL((paged_decode_kernel<D, kWideWaves, kStep>), dim3(p.Hkv, p.n_splits),
+                               dim3(kWideWaves * 64), 0, stream, p);
     }
     if (!wide)
-        hipLaunchKernelGGL((paged_decode_kernel<D, kWaves>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64), 0, stream, p);
+        hipLaunchKernelGGL((paged_decode_kernel<D, kWaves, kStep>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64), 0,
+                           stream, p);
+}
+
+template <int D>
+int launch_decode_d(const AttnParams& p, hipStream_t stream) {
+    if (p.step)
+        launch_split<D, true>(p, stream);
+    else
+        launch_split<D, false>(p, stream);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1 && !p.counters) {
         if (p.n_splits > 4 * kMergeU)

@@ -192,6 +192,18 @@ class PagedAttentionManager:
             raise ValueError(f"pool is {n} bytes, source {size}")
         copy_to_device(i.v_pool if which else i.k_pool, src)
 
+    # -- device-position decode (graph-capturable steps)
+    def stage_decode(self, layer: int, n_tokens: int, stream=None):
+        """Open the pages of the next n_tokens positions (as per-step appends
+        would) and hand the layer's position to the device."""
+        call("genllm_kv_stage_decode", self._h, layer, n_tokens, _stream(stream))
+
+    def sync_decode(self, layer: int, stream=None) -> int:
+        """Read the device position back (waits for `stream`); returns num_cached."""
+        n = C.c_int32()
+        call("genllm_kv_sync_decode", self._h, layer, _stream(stream), C.byref(n))
+        return n.value
+
     def read_device_table(self, layer: int):
         i = self.get_layer(layer)
         k = copy_to_host(i.k_ids, np.empty(i.num_pages, dtype=np.int32))
@@ -209,6 +221,24 @@ def paged_attention(mgr: PagedAttentionManager, layer: int, q, k, v, out, n_kv_g
         assert t.dtype == torch.bfloat16 and t.is_contiguous()
     call("genllm_paged_attention", mgr.handle, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, Hq, S, D, Hkv,
          n_kv_groups, float(scale), int(causal), _stream(stream))
+
+
+def paged_attention_step(mgr: PagedAttentionManager, layer: int, q, k, v, out, n_kv_groups: int, scale: float,
+                         causal: bool = True, stream=None):
+    """The op at the layer's device position (a staged layer; capturable)."""
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    for t in (q, k, v, out):
+        assert t.dtype == torch.bfloat16 and t.is_contiguous()
+    call("genllm_paged_attention_step", mgr.handle, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, Hq, S, D, Hkv,
+         n_kv_groups, float(scale), int(causal), _stream(stream))
+
+
+def apply_rope_step(mgr: PagedAttentionManager, layer: int, out, x, cos, sin, stream=None):
+    """apply_rope with start_pos = the staged layer's device position (capturable)."""
+    H, S, D = x.shape
+    call("genllm_apply_rope_step", mgr.handle, layer, _ptr(out), _ptr(x), _ptr(cos), _ptr(sin), H, S, D,
+         int(cos.shape[-1]), int(cos.shape[0]), _stream(stream))
 
 
 def qk_norm_rope_append(mgr: PagedAttentionManager, layer: int, k, v, gamma_k, eps: float, cos, sin,

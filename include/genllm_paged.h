@@ -125,6 +125,50 @@ int genllm_paged_attention(genllm_kv *kv, int32_t layer, const void *q, const vo
                            int32_t batch, int32_t n_q_heads, int32_t seq_len, int32_t head_dim,
                            int32_t n_kv_heads, int32_t n_kv_groups, float scale, int32_t causal, void *stream);
 
+/* ------------------------------------------ device-position decode steps
+ * The reference's decode loop advances the cache position every step
+ * (src/core/executor.cpp:227-236) and each step's append opens a page when the
+ * position reaches a multiple of 16 (append_kv_pages, page_attention.cpp:
+ * 141-162).  These calls move both to the device so that a decode step can be
+ * captured once into a HIP graph and replayed for successive tokens:
+ *
+ *   genllm_kv_stage_decode(kv, l, n, s)   host: open the pages positions
+ *       [end, end + n) need, in the order per-step appends would (same block
+ *       ids), and upload them; the first call also hands the position to the
+ *       device.  Later calls extend the window.  Not capturable (async copies
+ *       from pinned staging on s); run it before capture or between replays.
+ *   genllm_apply_rope_step / genllm_paged_attention_step   capturable: kernel
+ *       launches only, reading the position from the layer's device control
+ *       block; the attention step appends this step's K/V, attends, and its
+ *       last workgroup advances the position by seq_len.
+ *   genllm_kv_sync_decode(kv, l, s, &n)   host: waits for s, reads the
+ *       position back into num_cached and returns the staged blocks no step
+ *       reached, in reverse order, so that the layer (tables, pools, free
+ *       lists) is exactly what the same per-step appends would have left.
+ *
+ * While staged, num_cached / the page tables report the end of the window,
+ * and the host-driven calls (paged_attention, append_pages, set_page_table,
+ * block_alloc/free, qk_norm_rope_append) are refused with GENLLM_ERR_INVALID.
+ * A step whose tokens would pass the window (or, for the attention step, the
+ * window the step was planned for when it was captured) does nothing and
+ * raises the layer's error flag, which genllm_kv_sync_decode reports as
+ * GENLLM_ERR_POOL_FULL; later steps then do nothing either.  Steps of one layer
+ * must run in stream order (one stream, or a graph replayed on it). */
+int genllm_kv_stage_decode(genllm_kv *kv, int32_t layer, int32_t n_tokens, void *stream);
+int genllm_kv_sync_decode(genllm_kv *kv, int32_t layer, void *stream, int32_t *num_cached);
+/* PagedAttentionImpl::execute (attention.cpp:123-216) at the device position:
+ * arguments as genllm_paged_attention; seq_len * n_kv_groups <= 16. */
+int genllm_paged_attention_step(genllm_kv *kv, int32_t layer, const void *q, const void *k, const void *v,
+                                void *out, int32_t batch, int32_t n_q_heads, int32_t seq_len, int32_t head_dim,
+                                int32_t n_kv_heads, int32_t n_kv_groups, float scale, int32_t causal,
+                                void *stream);
+/* ApplyRopeImpl::execute (rope.cpp:76-119) with start_pos = the staged layer's
+ * device position; arguments as genllm_apply_rope, and max_seq = the rows of
+ * the cos/sin tables (a step past them raises the layer's error flag). */
+int genllm_apply_rope_step(genllm_kv *kv, int32_t layer, void *out, const void *x, const float *cos_tab,
+                           const float *sin_tab, int32_t n_heads, int32_t seq_len, int32_t head_dim,
+                           int32_t rope_dim, int32_t max_seq, void *stream);
+
 /* The Qwen3 layer's q/k per-head RMSNorm -> RoPE -> page scatter, fused
  * (src/model/Qwen3.cpp:137-166 = RmsNormImpl normalization.cpp:138-153, then
  * ApplyRopeImpl rope.cpp:76-119, then append_kv_from_tensor

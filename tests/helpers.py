@@ -41,8 +41,10 @@ def ulp_diff(a_bits, b_bits):
     return np.abs(key(a_bits) - key(b_bits))
 
 
-def oracle_fragmented(orc, Hkv, D, pool, perm_k, perm_v, layer=0):
-    m = orc.Manager(with_pool=True)
+def oracle_fragmented(orc, Hkv, D, pool, perm_k, perm_v, layer=0, m=None):
+    """Oracle manager (a new one, or layer `layer` added to `m`) whose block
+    pools hand out perm_k / perm_v first, as PagedAttentionManager.fragment."""
+    m = m if m is not None else orc.Manager(with_pool=True)
     m.init_layer(layer, Hkv, D)
     m.reserve_layer(layer, pool)
     for which, perm in ((0, perm_k), (1, perm_v)):
