@@ -55,6 +55,7 @@ constexpr int kWaves = 4;       // waves of a split workgroup (long page ranges)
 constexpr int kWideWaves = 8;   // waves of a split workgroup over short ranges (D = 128)
 constexpr int kWideMaxPps = 32; // pages per split up to which the 8-wave form runs
 constexpr int kMergeU = 16;     // splits in flight per merge lane
+constexpr int kMergeDims = 64;  // dims per merge workgroup
 constexpr int kMaxSplits = 256;
 // pages in flight per wave: 1 at D = 128 (a wave requests page j+1 only after
 // page j's data has arrived; measured faster than 2 or 3 at 8K and 32K keys:
@@ -543,47 +544,64 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     if (p.counters && p.n_splits > 1) merge_last_arrival<D, W>(p, h, lds_m, lds_l, lds_o);
 }
 
-// Merge of the splits: one workgroup of MW waves per (kv head, row), grid
-// (Hkv, rows) in the split grid's XCD order.  Wave w
+// Merge of the splits: one workgroup of MW waves per (kv head, row, 64-dim
+// block), grid (Hkv, rows, D / 64) in the split grid's XCD order.  Wave w
 // reduces the splits w, w+MW, ... to its own log-sum-exp partial (M_w, L_w,
-// O_w): each lane loads the o of its dims and, as a broadcast, the (m, l) of
+// O_w): each lane loads the o of its dim and, as a broadcast, the (m, l) of
 // each of those splits, up to kMergeU splits before any arithmetic (one memory
 // round trip for up to MW * kMergeU splits); the MW partials then meet in LDS
 // with the same rule
 //   M = max M_w, L = sum L_w 2^(M_w - M), O = sum O_w 2^(M_w - M), out = O / L.
 // MW is 4, or 8 above 4 * kMergeU splits (measured: 8 waves cost about 0.4 us
-// at 31-32 splits and save 0.6 us at 103).
+// at 31-32 splits and save 0.6 us at 103).  Blocks of 64 dims rather than one
+// workgroup per row (D dims) spread a row's partials over D / 64 CUs; on one
+// box, 128-dim blocks against 64: Qwen3.5 (D = 256, 103 splits) 12.8 -> 12.3
+// us per decode, config 3 13.1 -> 12.9 us (whole rows measured 14.2 us on the
+// Qwen3.5 shape, on a box where config 3 took 13.6).
 template <int D, int MW>
 __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams p) {
-    constexpr int kMergeWaves = MW;
-    constexpr int U = kMergeU;   // splits in flight per lane
-    constexpr int VH = D / 128;  // lane -> dims 128 hh + 2 lane, +1
-    __shared__ float s_o[kMergeWaves][D];
-    __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
+    constexpr int U = kMergeU;  // splits in flight per lane
+    constexpr int PL = 1;       // dims per lane (the workgroup's kMergeDims dims)
+    static_assert(kMergeDims == 64 * PL, "merge: one lane per dim group");
+    __shared__ float s_o[MW][kMergeDims];
+    __shared__ float s_m[MW], s_l[MW];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int h = blockIdx.x, ri = blockIdx.y;
+    const int h = blockIdx.x, ri = blockIdx.y, d0 = kMergeDims * int(blockIdx.z);
     // device-position step refused by the split kernel: no partials to merge
     if (p.step && step_load(p.step + kStepError)) return;
     const int rows = p.G * p.S;
     const int ns = p.n_splits;  // <= kMaxSplits
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
                        int64_t(h) * ns * rows + ri;
-    const float* po = p.partial + (int64_t(h) * ns * rows + ri) * D + 2 * lane;
+    const float* po = p.partial + (int64_t(h) * ns * rows + ri) * D + d0 + PL * lane;
     const int64_t sstride = int64_t(rows) * D;  // floats between splits
+    auto load_o = [&](int s2, float (&o)[PL]) {
+        if constexpr (PL == 2) {
+            const float2 v = *reinterpret_cast<const float2*>(po + s2 * sstride);
+            o[0] = v.x;
+            o[1] = v.y;
+        } else {
+            o[0] = po[s2 * sstride];
+        }
+    };
 
-    float mw = -INFINITY, lw = 0.0f, o0[VH], o1[VH];
+    float mw = -INFINITY, lw = 0.0f, ow[PL];
 #pragma unroll
-    for (int hh = 0; hh < VH; ++hh) o0[hh] = o1[hh] = 0.0f;
-    for (int s0 = wv; s0 < ns; s0 += kMergeWaves * U) {
-        float2 ov[U][VH], mv[U];
+    for (int e = 0; e < PL; ++e) ow[e] = 0.0f;
+    for (int s0 = wv; s0 < ns; s0 += MW * U) {
+        float ov[U][PL];
+        float2 mv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int s2 = s0 + kMergeWaves * u;
+            const int s2 = s0 + MW * u;
+            if (s2 < ns) {
+                load_o(s2, ov[u]);
+                mv[u] = ml[s2 * rows];
+            } else {
 #pragma unroll
-            for (int hh = 0; hh < VH; ++hh)
-                ov[u][hh] = s2 < ns ? *reinterpret_cast<const float2*>(po + s2 * sstride + 128 * hh)
-                                    : make_float2(0.0f, 0.0f);
-            mv[u] = s2 < ns ? ml[s2 * rows] : make_float2(-INFINITY, 0.0f);
+                for (int e = 0; e < PL; ++e) ov[u][e] = 0.0f;
+                mv[u] = make_float2(-INFINITY, 0.0f);
+            }
         }
         float bm = mw;
 #pragma unroll
@@ -592,27 +610,18 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
         const float a = mw == -INFINITY ? 0.0f : exp2_fast(mw - bm);
         lw *= a;
 #pragma unroll
-        for (int hh = 0; hh < VH; ++hh) {
-            o0[hh] *= a;
-            o1[hh] *= a;
-        }
+        for (int e = 0; e < PL; ++e) ow[e] *= a;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const float w = mv[u].x == -INFINITY ? 0.0f : exp2_fast(mv[u].x - bm);
             lw += mv[u].y * w;
 #pragma unroll
-            for (int hh = 0; hh < VH; ++hh) {
-                o0[hh] += ov[u][hh].x * w;
-                o1[hh] += ov[u][hh].y * w;
-            }
+            for (int e = 0; e < PL; ++e) ow[e] += ov[u][e] * w;
         }
         mw = bm;
     }
 #pragma unroll
-    for (int hh = 0; hh < VH; ++hh) {
-        s_o[wv][128 * hh + 2 * lane] = o0[hh];
-        s_o[wv][128 * hh + 2 * lane + 1] = o1[hh];
-    }
+    for (int e = 0; e < PL; ++e) s_o[wv][PL * lane + e] = ow[e];
     if (lane == 0) {
         s_m[wv] = mw;
         s_l[wv] = lw;
@@ -621,26 +630,24 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
     if (wv == 0) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w2 = 0; w2 < kMergeWaves; ++w2) M = fmaxf(M, s_m[w2]);
-        float L = 0.0f, O0[VH], O1[VH];
+        for (int w2 = 0; w2 < MW; ++w2) M = fmaxf(M, s_m[w2]);
+        float L = 0.0f, O[PL];
 #pragma unroll
-        for (int hh = 0; hh < VH; ++hh) O0[hh] = O1[hh] = 0.0f;
+        for (int e = 0; e < PL; ++e) O[e] = 0.0f;
 #pragma unroll
-        for (int w2 = 0; w2 < kMergeWaves; ++w2) {
-            const float e = s_m[w2] == -INFINITY ? 0.0f : exp2_fast(s_m[w2] - M);
-            L += s_l[w2] * e;
+        for (int w2 = 0; w2 < MW; ++w2) {
+            const float f = s_m[w2] == -INFINITY ? 0.0f : exp2_fast(s_m[w2] - M);
+            L += s_l[w2] * f;
 #pragma unroll
-            for (int hh = 0; hh < VH; ++hh) {
-                O0[hh] += s_o[w2][128 * hh + 2 * lane] * e;
-                O1[hh] += s_o[w2][128 * hh + 2 * lane + 1] * e;
-            }
+            for (int e = 0; e < PL; ++e) O[e] += s_o[w2][PL * lane + e] * f;
         }
         const float inv = 1.0f / L;
-        uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride;
-#pragma unroll
-        for (int hh = 0; hh < VH; ++hh)
-            *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
-                pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
+        uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride +
+                         d0 + PL * lane;
+        if constexpr (PL == 2)
+            *reinterpret_cast<uint32_t*>(orow) = pack2(f32_to_bf16_ref(O[0] * inv), f32_to_bf16_ref(O[1] * inv));
+        else
+            *orow = uint16_t(f32_to_bf16_ref(O[0] * inv));
     }
 }
 
@@ -723,10 +730,11 @@ int launch_decode_d(const AttnParams& p, hipStream_t stream) {
         launch_split<D, false>(p, stream);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1 && !p.counters) {
+        const dim3 grid(p.Hkv, p.G * p.S, D / kMergeDims);
         if (p.n_splits > 4 * kMergeU)
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), dim3(p.Hkv, p.G * p.S), dim3(8 * 64), 0, stream, p);
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), grid, dim3(8 * 64), 0, stream, p);
         else
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4>), dim3(p.Hkv, p.G * p.S), dim3(4 * 64), 0, stream, p);
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4>), grid, dim3(4 * 64), 0, stream, p);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;
