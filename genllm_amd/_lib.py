@@ -83,6 +83,7 @@ SIGNATURES = {
     "genllm_kv_block_alloc": (_int, [_P, _i32, _i32, C.POINTER(_i32)]),
     "genllm_kv_block_free": (_int, [_P, _i32, _i32, _i32]),
     "genllm_paged_attention": (_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, _i32, _P]),
+    "genllm_kv_append_from_pos": (_int, [_P, _i32, _P, _P, _i32, _i32, _i32, _i32, _i32, _P]),
     "genllm_kv_stage_decode": (_int, [_P, _i32, _i32, _P]),
     "genllm_kv_sync_decode": (_int, [_P, _i32, _P, _P]),
     "genllm_paged_attention_step": (_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, _i32,

@@ -948,6 +948,75 @@ extern "C" int genllm_rope_cache(float* dst, float theta, int32_t head_dim, int3
     return GENLLM_OK;
 }
 
+// append_kv_from_pos (page_attention.cpp:164-203) as a manager call: the
+// pages of positions [global_pos, global_pos + count) are opened by the rule
+// of append_kv_pages (a block from each pool at every position that is a
+// multiple of 16, entered into the table only past its end), the rows are
+// written by the scatter kernel, and num_cached = max(num_cached,
+// global_pos + count).  The source is head-major [Hkv][count][D] for every
+// head (the reference reads head 0's row for all heads, :195 and :198).
+// Checked before anything changes: every touched page must exist after the
+// call (no gap past the table end, none not opened by this call), and both
+// pools must hold the pages it opens.
+extern "C" int genllm_kv_append_from_pos(genllm_kv* kv, int32_t layer, const void* k, const void* v,
+                                         int32_t n_kv_heads, int32_t head_dim, int32_t dtype, int32_t global_pos,
+                                         int32_t count, void* stream) {
+    if (!kv) return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: null kv");
+    LayerState* s = active_layer(kv, layer);
+    if (!s) return GENLLM_OK;  // page_attention.cpp:169: inactive layer
+    if (int rc = refuse_staged(*s, "append_kv_from_pos")) return rc;
+    if (count <= 0) return GENLLM_OK;
+    if (!s->k_base) return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: layer has no reserved pools");
+    if (!k || !v) return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: null k/v");
+    if (dtype != s->dtype || elem_size(dtype) != 2 || n_kv_heads != s->n_kv_heads || head_dim != s->head_dim)
+        return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: tensor shape/dtype differs from the layer's pools");
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail(GENLLM_ERR_UNSUPPORTED, "append_kv_from_pos: head_dim must be 64, 128 or 256");
+    if (!aligned(k, 16) || !aligned(v, 16))
+        return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: k/v must be 16-byte aligned");
+    if (global_pos < 0 || int64_t(global_pos) + count > int64_t(INT32_MAX) - kPage)
+        return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: position out of range");
+    const int64_t size = int64_t(s->k_ids.size());
+    const int64_t first = (int64_t(global_pos) + kPage - 1) / kPage;  // first page this call opens
+    const int64_t need = pages_opened(global_pos, count);
+    const int64_t new_size = need > 0 ? std::max(size, first + need) : size;
+    const int64_t last = (int64_t(global_pos) + count - 1) / kPage;  // last page written
+    if ((need > 0 && first > size) || last >= new_size)
+        return fail(GENLLM_ERR_INVALID, "append_kv_from_pos: positions " + std::to_string(global_pos) + ".." +
+                                            std::to_string(int64_t(global_pos) + count - 1) +
+                                            " reach pages the table does not hold and this call does not open");
+    hipStream_t st = as_stream(stream);
+    const int32_t saved = s->num_cached;
+    AppendUndo& undo = t_undo;
+    s->num_cached = global_pos;  // append_pages opens pages from its layer's num_cached
+    if (int rc = append_pages(kv, *s, count, st, static_cast<TableUpdate*>(nullptr), &undo)) {
+        s->num_cached = saved;
+        return rc;
+    }
+    s->num_cached = std::max(saved, global_pos + count);
+    AppendParams ap;
+    ap.k = static_cast<const uint16_t*>(k);
+    ap.v = static_cast<const uint16_t*>(v);
+    ap.k_tok_stride = ap.v_tok_stride = head_dim;
+    ap.k_head_stride = ap.v_head_stride = int64_t(count) * head_dim;
+    ap.S = count;
+    ap.Hkv = n_kv_heads;
+    ap.pos0 = global_pos;
+    ap.nkv_tasks = (n_kv_heads + 7) / 8;
+    ap.k_pool = s->k_base;
+    ap.v_pool = s->v_base;
+    ap.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
+    ap.k_ids = s->d_k_ids;
+    ap.v_ids = s->d_v_ids;
+    ap.max_blocks = s->max_blocks;
+    if (int rc = launch_kv_append(ap, head_dim, st)) {
+        undo_append(*s, undo);
+        s->num_cached = saved;
+        return rc;
+    }
+    return GENLLM_OK;
+}
+
 extern "C" int genllm_kv_scatter(const void* k, int64_t k_tok_stride, int64_t k_head_stride, const void* v,
                                  int64_t v_tok_stride, int64_t v_head_stride, void* k_pool, void* v_pool,
                                  const int32_t* k_ids, const int32_t* v_ids, int32_t pos0, int32_t seq_len,

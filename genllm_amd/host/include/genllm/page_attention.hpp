@@ -74,6 +74,10 @@ public:
     // :104-140 -- K_data/V_data are device pointers, head-major [n_kv_heads][seq_len][head_dim]
     void append_kv_from_tensor(int32_t layer_id, const void* K_data, const void* V_data, int32_t n_kv_heads,
                                int32_t seq_len, int32_t head_dim, DataType dtype);
+    // :164-203 -- K_data/V_data device pointers, head-major [n_kv_heads][count][head_dim] (every head
+    // reads its own rows; the reference reads head 0's for all); errors leave the layer unchanged
+    void append_kv_from_pos(int32_t layer_id, const void* K_data, const void* V_data, int32_t n_kv_heads,
+                            int32_t head_dim, DataType dtype, int32_t global_pos, int32_t count);
     void append_kv_pages(int32_t layer_id, int32_t count);                                          // :141-162
     void reset();                                                                                   // :208-216
     bool is_active(int32_t layer_id) const;                                                         // .h:82-85

@@ -110,6 +110,14 @@ void PagedAttentionManager::append_kv_from_tensor(int32_t layer_id, const void* 
                  "append_kv_from_tensor");
 }
 
+void PagedAttentionManager::append_kv_from_pos(int32_t layer_id, const void* K_data, const void* V_data,
+                                               int32_t n_kv_heads, int32_t head_dim, DataType dtype,
+                                               int32_t global_pos, int32_t count) {
+    genllm_check(genllm_kv_append_from_pos(kv_, layer_id, K_data, V_data, n_kv_heads, head_dim, int32_t(dtype),
+                                           global_pos, count, stream_),
+                 "append_kv_from_pos");
+}
+
 void PagedAttentionManager::append_kv_pages(int32_t layer_id, int32_t count) {
     genllm_check(genllm_kv_append_pages(kv_, layer_id, count, stream_), "append_kv_pages");
 }

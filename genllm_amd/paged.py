@@ -125,6 +125,14 @@ class PagedAttentionManager:
     def append_kv_pages(self, layer: int, count: int, stream=None):
         call("genllm_kv_append_pages", self._h, layer, count, _stream(stream))
 
+    def append_kv_from_pos(self, layer: int, k, v, global_pos: int, stream=None):
+        """append_kv_from_pos: k, v device bf16 head-major [Hkv][count][D]."""
+        Hkv, count, D = k.shape
+        for t in (k, v):
+            assert t.dtype == torch.bfloat16 and t.is_contiguous()
+        call("genllm_kv_append_from_pos", self._h, layer, _ptr(k), _ptr(v), Hkv, D, DTYPE_BF16, global_pos, count,
+             _stream(stream))
+
     def reset(self):
         call("genllm_kv_reset", self._h)
 

@@ -72,6 +72,19 @@ int genllm_kv_is_active(genllm_kv *kv, int32_t layer, int32_t *active);
  * without enough free pages returns GENLLM_ERR_POOL_FULL and leaves the layer
  * unchanged. */
 int genllm_kv_append_pages(genllm_kv *kv, int32_t layer, int32_t count, void *stream);
+/* PagedAttentionManager::append_kv_from_pos, page_attention.cpp:164-203: write
+ * count tokens at positions global_pos.. (k, v: device, head-major
+ * [n_kv_heads][count][head_dim], dtype the layer's 2-byte type), opening pages
+ * by the rule of append_kv_pages (a K and a V block at every position that is
+ * a multiple of 16, entered into the table only past its end), then
+ * num_cached = max(num_cached, global_pos + count).  Every head reads its own
+ * rows: the reference copies head 0's row p to every head (:195, :198).
+ * Errors leave the layer unchanged: GENLLM_ERR_INVALID when a position's page
+ * is neither in the table nor opened by this call (the reference indexes the
+ * table unchecked there), GENLLM_ERR_POOL_FULL when a pool cannot supply the
+ * pages (the reference stops part-way).  count <= 0 does nothing. */
+int genllm_kv_append_from_pos(genllm_kv *kv, int32_t layer, const void *k, const void *v, int32_t n_kv_heads,
+                              int32_t head_dim, int32_t dtype, int32_t global_pos, int32_t count, void *stream);
 /* PagedAttentionManager::reset (page_attention.cpp:208-216), reached through
  * MemoryManager::reset_kv_cache (manager.cpp:97-101). Host-only. */
 int genllm_kv_reset(genllm_kv *kv);

@@ -69,6 +69,7 @@ def _declare(L):
         "or_mgr_reserve_layer": (None, [_P, _i32, _i32]),
         "or_mgr_append_kv_pages": (None, [_P, _i32, _i32]),
         "or_mgr_append_kv_from_tensor": (None, [_P, _i32, _P, _P, _i32, _i32, _i32, _i32]),
+        "or_mgr_append_kv_from_pos": (None, [_P, _i32, _P, _P, _i32, _i32, _i32, _i32, _i32]),
         "or_mgr_reset": (None, [_P]),
         "or_mgr_is_active": (C.c_int, [_P, _i32]),
         "or_mgr_num_cached": (_i32, [_P, _i32]),
@@ -254,6 +255,13 @@ class Manager:
         V = np.ascontiguousarray(V, dtype=np.uint16)
         Hkv, S, D = K.shape
         lib().or_mgr_append_kv_from_tensor(self._h, layer, ptr(K), ptr(V), Hkv, S, D, BF16)
+
+    def append_kv_from_pos(self, layer, K, V, global_pos):
+        """K/V head-major [Hkv][count][D]."""
+        K = np.ascontiguousarray(K, dtype=np.uint16)
+        V = np.ascontiguousarray(V, dtype=np.uint16)
+        Hkv, count, D = K.shape
+        lib().or_mgr_append_kv_from_pos(self._h, layer, ptr(K), ptr(V), Hkv, D, BF16, global_pos, count)
 
     def reset(self):
         lib().or_mgr_reset(self._h)

@@ -78,6 +78,8 @@ void or_mgr_reserve_layer(or_manager *m, int32_t layer, int32_t max_blocks);
 void or_mgr_append_kv_pages(or_manager *m, int32_t layer, int32_t count);
 void or_mgr_append_kv_from_tensor(or_manager *m, int32_t layer, const void *K, const void *V,
                                   int32_t n_kv_heads, int32_t seq_len, int32_t head_dim, int32_t dtype);
+void or_mgr_append_kv_from_pos(or_manager *m, int32_t layer, const void *K, const void *V, int32_t n_kv_heads,
+                               int32_t head_dim, int32_t dtype, int32_t global_pos, int32_t count);
 void or_mgr_reset(or_manager *m);
 int or_mgr_is_active(const or_manager *m, int32_t layer);
 int32_t or_mgr_num_cached(or_manager *m, int32_t layer);

@@ -241,6 +241,48 @@ void or_mgr_append_kv_from_tensor(or_manager *m, int32_t layer, const void *K, c
     }
 }
 
+/* append_kv_from_pos -- :164-203.  The reference's loop over the positions
+ * g = global_pos + p: at every g with g % 16 == 0 a block is taken from each
+ * pool (the loop stops when one is exhausted) and entered into the table only
+ * past its end, as append_kv_pages does; row p is written to page
+ * table[g/16], slot g%16; at the end num_cached = max(num_cached,
+ * global_pos + count).  Two departures, both where the reference has
+ * undefined or wrong behaviour: the source row of head h is
+ * K + (h*count + p)*D, head-major [Hkv][count][D] as append_kv_from_tensor
+ * reads it (the reference reads K + p*D for every head, :195 and :198), and a
+ * position whose page is not in the table stops the loop (the reference
+ * indexes page_table[g/16] unchecked). */
+void or_mgr_append_kv_from_pos(or_manager *m, int32_t layer, const void *K, const void *V, int32_t n_kv_heads,
+                               int32_t head_dim, int32_t dtype, int32_t global_pos, int32_t count) {
+    or_layer *s = get_layer(m, layer);
+    if (!s->active) return;
+    size_t es = dtype_size(dtype);
+    size_t row = (size_t)head_dim * es;
+    size_t head_stride = (size_t)(count > 0 ? count : 0) * row;
+    for (int32_t p = 0; p < count; ++p) {
+        int32_t g = global_pos + p;
+        int32_t lb = g / OR_PAGE_BLOCK_SIZE;
+        int32_t off = g % OR_PAGE_BLOCK_SIZE;
+        if (off == 0) {
+            int32_t k_id = or_pool_alloc(&s->k_pool);
+            int32_t v_id = or_pool_alloc(&s->v_pool);
+            if (k_id < 0 || v_id < 0) break;
+            if (lb >= s->n_pages) table_push(s, k_id, v_id);
+        }
+        if (lb >= s->n_pages) break;
+        uint8_t *kb = (uint8_t *)or_pool_block_data(&s->k_pool, s->k_ids[lb]);
+        uint8_t *vb = (uint8_t *)or_pool_block_data(&s->v_pool, s->v_ids[lb]);
+        if (!kb || !vb) continue;
+        uint8_t *kd = kb + (size_t)off * (size_t)n_kv_heads * row;
+        uint8_t *vd = vb + (size_t)off * (size_t)n_kv_heads * row;
+        for (int32_t h = 0; h < n_kv_heads; ++h) {
+            memcpy(kd + (size_t)h * row, (const uint8_t *)K + (size_t)h * head_stride + (size_t)p * row, row);
+            memcpy(vd + (size_t)h * row, (const uint8_t *)V + (size_t)h * head_stride + (size_t)p * row, row);
+        }
+    }
+    if (global_pos + count > s->num_cached) s->num_cached = global_pos + count;
+}
+
 /* reset -- :208-216 */
 void or_mgr_reset(or_manager *m) {
     for (int32_t i = 0; i < m->n_layers; ++i) {

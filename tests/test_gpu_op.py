@@ -252,3 +252,62 @@ def test_reserve_fits_exact_scheduler_sizing(orc):
         short.reserve_layer(L - 1, max_blocks)
     assert e.value.code == ERR_NO_MEMORY
     short.close()
+
+
+def test_append_kv_from_pos_matches_oracle(orc):
+    """append_kv_from_pos (page_attention.cpp:164-203) through the product
+    manager against the oracle: writing from position 0, rewriting positions
+    inside the cache across a multiple of 16 (a block is still taken there),
+    extending past the end (page opened at 48), an unaligned append that opens
+    the page at 64; then the refusals -- a position whose page is neither in
+    the table nor opened by the call, a pool without enough pages -- leave the
+    layer as it was; finally a decode step attends over the rewritten cache."""
+    Hq, Hkv, D, pool = 32, 8, 128, 8
+    mgr, ref = make(orc, Hkv, D, pool, 7070)
+
+    def put(g0, count, seed):
+        K = synth.normal_bf16(seed, (Hkv, count, D))
+        V = synth.normal_bf16(seed + 1, (Hkv, count, D))
+        print(f"append_kv_from_pos({g0}, {count})", flush=True)
+        mgr.append_kv_from_pos(0, paged.to_device_bf16(K), paged.to_device_bf16(V), g0)
+        ref.append_kv_from_pos(0, K, V, g0)
+
+    def same(label):
+        torch.cuda.synchronize()
+        info = mgr.get_layer(0)
+        assert info.num_cached == ref.num_cached(0), label
+        kt, vt = mgr.page_table(0)
+        rk, rv = ref.page_table(0)
+        assert np.array_equal(kt, rk) and np.array_equal(vt, rv), label
+        assert (info.k_num_blocks, info.k_num_free) == (ref.pool(0, 0).num_blocks(), ref.pool(0, 0).num_free())
+        assert (info.v_num_blocks, info.v_num_free) == (ref.pool(0, 1).num_blocks(), ref.pool(0, 1).num_free())
+        assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0)), label
+        assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1)), label
+        dk, dv = mgr.read_device_table(0)
+        assert np.array_equal(dk, rk) and np.array_equal(dv, rv), label
+
+    put(0, 40, 10)
+    same("write 0..39")
+    put(10, 9, 20)
+    same("rewrite 10..18")
+    put(40, 13, 30)
+    same("extend 40..52")
+    put(53, 20, 40)
+    same("append 53..72")
+
+    before = (mgr.get_layer(0).num_cached, mgr.page_table(0), mgr.read_pool(0, 0))
+    K = paged.to_device_bf16(synth.normal_bf16(50, (Hkv, 5, D)))
+    with pytest.raises(GenllmError) as e:  # page 6 (position 100) is not in the 5-page table
+        mgr.append_kv_from_pos(0, K, K, 100)
+    assert e.value.code == ERR_INVALID
+    K2 = paged.to_device_bf16(synth.normal_bf16(51, (Hkv, 60, D)))
+    with pytest.raises(GenllmError) as e:  # 80..139 takes 4 blocks per pool; 2 are left (6 of 8 taken)
+        mgr.append_kv_from_pos(0, K2, K2, 80)
+    assert e.value.code == ERR_POOL_FULL
+    torch.cuda.synchronize()
+    after = (mgr.get_layer(0).num_cached, mgr.page_table(0), mgr.read_pool(0, 0))
+    assert before[0] == after[0] and np.array_equal(before[1][0], after[1][0])
+    assert np.array_equal(before[2], after[2])
+    same("after the refusals")
+    step(mgr, ref, 0, Hq, Hkv, 1, D, 60, "decode over the rewritten cache")
+    mgr.close()

@@ -293,6 +293,75 @@ def test_append_page_placement_closed_form(orc):
     assert not kp[k_ids[-1], last:].any() and not vp[v_ids[-1], last:].any()
 
 
+def test_append_from_pos_at_the_end_equals_append_from_tensor(orc):
+    """append_kv_from_pos(num_cached, ...) opens the same pages, in the same
+    order, and writes the same rows as append_kv_from_tensor (both loops of
+    page_attention.cpp take a block at every position that is a multiple of
+    16 and push it past the table end); num_cached ends the same."""
+    Hkv, D, pool = 3, 16, 12
+    perm_k, perm_v = synth.shuffled(3, pool), synth.shuffled(4, pool)
+    a = fragmented(orc, Hkv, D, pool, perm_k, perm_v)
+    b = fragmented(orc, Hkv, D, pool, perm_k, perm_v)
+    pos = 0
+    for S in [5, 11, 1, 16, 20, 3]:
+        K = synth.normal_bf16(300 + S, (Hkv, S, D))
+        V = synth.normal_bf16(400 + S, (Hkv, S, D))
+        a.append_kv_from_tensor(0, K, V)
+        b.append_kv_from_pos(0, K, V, pos)
+        pos += S
+        assert a.num_cached(0) == b.num_cached(0) == pos
+        ka, va = a.page_table(0)
+        kb, vb = b.page_table(0)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+        for which in (0, 1):
+            assert a.pool(0, which).num_blocks() == b.pool(0, which).num_blocks()
+            assert a.pool(0, which).num_free() == b.pool(0, which).num_free()
+            assert np.array_equal(a.pool_array(0, which), b.pool_array(0, which))
+
+
+def test_append_from_pos_rewrite_closed_form(orc):
+    """Positions below num_cached are rewritten in place: row t of head h lands
+    at table[g/16] slot g%16 head h (g = global_pos + t), every head from its
+    own source rows; a position that is a multiple of 16 still takes a block
+    from each pool, entered into the table only past its end (:178-184), so
+    the pools' counts move exactly by the multiples of 16 crossed; num_cached
+    = max(num_cached, global_pos + count)."""
+    Hkv, D, pool = 4, 16, 16
+    perm_k, perm_v = synth.shuffled(5, pool), synth.shuffled(6, pool)
+    m = fragmented(orc, Hkv, D, pool, perm_k, perm_v)
+    m.append_kv_from_tensor(0, synth.normal_bf16(7, (Hkv, 40, D)), synth.normal_bf16(8, (Hkv, 40, D)))
+    k_ids, v_ids = m.page_table(0)
+    before = [m.pool_array(0, w).copy() for w in (0, 1)]
+    free0 = m.pool(0, 0).num_free()
+    g0, count = 10, 9  # positions 10..18 cross the multiple of 16 at 16
+    K = synth.normal_bf16(9, (Hkv, count, D))
+    V = synth.normal_bf16(10, (Hkv, count, D))
+    m.append_kv_from_pos(0, K, V, g0)
+    assert m.num_cached(0) == 40
+    k2, v2 = m.page_table(0)
+    assert np.array_equal(k2, k_ids) and np.array_equal(v2, v_ids)  # no page pushed
+    assert m.pool(0, 0).num_free() == free0 - 1  # one block taken at position 16
+    want = [before[0].copy(), before[1].copy()]
+    for t in range(count):
+        g = g0 + t
+        for h in range(Hkv):
+            want[0][k_ids[g // 16], g % 16, h] = K[h, t]
+            want[1][v_ids[g // 16], g % 16, h] = V[h, t]
+    assert np.array_equal(m.pool_array(0, 0), want[0])
+    assert np.array_equal(m.pool_array(0, 1), want[1])
+    # past the end: 40..52 opens the page at 48, num_cached grows to 53
+    K = synth.normal_bf16(11, (Hkv, 13, D))
+    V = synth.normal_bf16(12, (Hkv, 13, D))
+    m.append_kv_from_pos(0, K, V, 40)
+    assert m.num_cached(0) == 53
+    k3, _ = m.page_table(0)
+    # the block taken at position 16 above stays taken: the new page is the next id
+    assert list(k3) == list(perm_k[:3]) + [perm_k[4]]
+    for t in range(13):
+        g = 40 + t
+        assert np.array_equal(m.pool_array(0, 0)[k3[g // 16], g % 16], K[:, t])
+
+
 # -------------------------------------------------------------- attention
 def brute_attention(q, K, V, groups, scale, causal, n_cached):
     """float64 softmax(q K^T scale) V; q [Hq][S][D], K/V [Hkv][N][D] (float)."""
