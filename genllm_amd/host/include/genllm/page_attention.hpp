@@ -11,6 +11,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <set>
 #include <vector>
 
 #include "genllm/tensor.hpp"
@@ -80,6 +81,15 @@ public:
                             int32_t head_dim, DataType dtype, int32_t global_pos, int32_t count);
     void append_kv_pages(int32_t layer_id, int32_t count);                                          // :141-162
     void reset();                                                                                   // :208-216
+    // Device-position decode for a HIP-graph-captured decode loop (no counterpart
+    // in the reference, whose executor advances the position on the host,
+    // executor.cpp:227-236): stage_decode opens the pages of the next n_tokens
+    // positions and hands the layer's position to the device; while a layer is
+    // staged, its PagedAttentionImpl / ApplyRopeImpl nodes take the position from
+    // the device (capturable); sync_decode reads it back and returns num_cached.
+    void stage_decode(int32_t layer_id, int32_t n_tokens);
+    int32_t sync_decode(int32_t layer_id);
+    bool is_staged(int32_t layer_id) const { return staged_.count(layer_id) != 0; }
     bool is_active(int32_t layer_id) const;                                                         // .h:82-85
 
     genllm_kv* handle() const { return kv_; }
@@ -93,6 +103,7 @@ private:
     genllm_kv* kv_ = nullptr;
     int32_t device_ = 0;
     void* stream_ = nullptr;
+    std::set<int32_t> staged_;
 };
 
 // Throws std::runtime_error carrying genllm_last_error() when status != 0.

@@ -52,9 +52,10 @@ void PagedAttentionImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     const float scale = out->op_params[1];
     const bool causal = int32_t(out->op_params[2]) != 0;
 
-    genllm_check(genllm_paged_attention(mgr->handle(), layer_id, Q->data, K->data, V->data, out->data, batch,
-                                        num_q_heads, seq_len, head_dim, num_kv_heads, num_kv_groups, scale,
-                                        causal ? 1 : 0, mgr->stream()),
+    // a staged layer (device-position decode) reads its position on the device
+    auto* const entry = mgr->is_staged(layer_id) ? genllm_paged_attention_step : genllm_paged_attention;
+    genllm_check(entry(mgr->handle(), layer_id, Q->data, K->data, V->data, out->data, batch, num_q_heads, seq_len,
+                       head_dim, num_kv_heads, num_kv_groups, scale, causal ? 1 : 0, mgr->stream()),
                  "paged_attention");
 }
 
@@ -112,6 +113,18 @@ void ApplyRopeImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     const int64_t start_pos = int64_t(out->op_params[2]);
     const int64_t B = x->dims[0], n_heads = x->dims[1], seq_len = x->dims[2];
     if (B != 1) throw std::runtime_error("apply_rope: batch must be 1");  // rope.cpp:89 asserts it
+    // a node of a staged layer takes start_pos from the device position
+    auto* mgr = g_mem_manager && out->layer_id >= 0 ? g_mem_manager->get_attention_manager(out->device, size_t(dev_id))
+                                                    : nullptr;
+    if (mgr && mgr->is_staged(out->layer_id)) {
+        const int64_t max_seq = int64_t(cos->num_elements()) / rope_dim;
+        genllm_check(genllm_apply_rope_step(mgr->handle(), out->layer_id, out->data, x->data,
+                                            static_cast<const float*>(cos->data), static_cast<const float*>(sin->data),
+                                            int32_t(n_heads), int32_t(seq_len), int32_t(head_dim), int32_t(rope_dim),
+                                            int32_t(max_seq), mgr->stream()),
+                     "apply_rope");
+        return;
+    }
     genllm_check(genllm_apply_rope(out->data, x->data, static_cast<const float*>(cos->data),
                                    static_cast<const float*>(sin->data), int32_t(n_heads), int32_t(seq_len),
                                    int32_t(head_dim), int32_t(rope_dim), start_pos, device_stream(out, dev_id)),

@@ -122,7 +122,23 @@ void PagedAttentionManager::append_kv_pages(int32_t layer_id, int32_t count) {
     genllm_check(genllm_kv_append_pages(kv_, layer_id, count, stream_), "append_kv_pages");
 }
 
-void PagedAttentionManager::reset() { genllm_check(genllm_kv_reset(kv_), "reset"); }
+void PagedAttentionManager::reset() {
+    genllm_check(genllm_kv_reset(kv_), "reset");
+    staged_.clear();  // the native reset leaves every layer host-driven
+}
+
+void PagedAttentionManager::stage_decode(int32_t layer_id, int32_t n_tokens) {
+    genllm_check(genllm_kv_stage_decode(kv_, layer_id, n_tokens, stream_), "stage_decode");
+    staged_.insert(layer_id);
+}
+
+int32_t PagedAttentionManager::sync_decode(int32_t layer_id) {
+    int32_t n = 0;
+    const int rc = genllm_kv_sync_decode(kv_, layer_id, stream_, &n);
+    staged_.erase(layer_id);  // synced even when it reports a refused step
+    genllm_check(rc, "sync_decode");
+    return n;
+}
 
 bool PagedAttentionManager::is_active(int32_t layer_id) const {
     int32_t a = 0;

@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <memory>
 #include <stdexcept>
 #include <vector>
 
@@ -263,6 +264,141 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
     return ok;
 }
 
+// A decode loop captured into one HIP graph (the executor's loop,
+// executor.cpp:227-236, without its per-step host bookkeeping): two layers'
+// RoPE(q), RoPE(k) and PAGED_ATTN nodes, their op_params' start_pos left
+// stale, dispatched once under stream capture with the layers staged, then
+// replayed for 12 tokens across the page boundary at 32.  Every replay:
+// RoPE'd q bit-exact and attention within tolerance of the oracle run with
+// host positions; after sync_decode, num_cached and the tables equal the
+// oracle's.
+bool test_decode_step_graph() {
+    const int32_t Hq = 32, Hkv = 8, D = 128, G = Hq / Hkv, L = 2, P = 26, steps = 12, max_seq = 128;
+    const float scale = 1.0f / std::sqrt(float(D));
+    MemoryManager mm;
+    hipStream_t s = nullptr;
+    ASSERT(hipStreamCreate(&s) == hipSuccess, "stream");
+    std::vector<Tensor> ks(L), sizing(L);
+    std::vector<Tensor*> graph;
+    for (int l = 0; l < L; ++l) {
+        ks[l] = make_tensor(nullptr, {1, Hkv, 1, D});
+        sizing[l] = make_tensor(nullptr, {1, Hq, 1, D});
+        sizing[l].op_type = OperationType::OP_TYPE_PAGED_ATTN;
+        sizing[l].src[1] = &ks[l];
+        sizing[l].layer_id = l;
+        graph.push_back(&sizing[l]);
+    }
+    PagedAttentionManager& pam =
+        mm.create_attention_manager(Device::HIP, 0, kv_cache_bytes(graph, Device::HIP, max_seq));
+    initialize_kv_cache(pam, graph, max_seq);
+    mm.set_stream(Device::HIP, 0, s);
+    or_manager* ref = or_mgr_create(1);
+    for (int l = 0; l < L; ++l) {
+        or_mgr_init_layer(ref, l, Hkv, D, OR_DTYPE_BF16);
+        or_mgr_reserve_layer(ref, l, (max_seq + 15) / 16);
+    }
+    bool ok = true;
+    // the prompt, through the host-position op
+    for (int l = 0; l < L; ++l) {
+        DevBuf q(size_t(Hq) * P * D * 2), k(size_t(Hkv) * P * D * 2), v(size_t(Hkv) * P * D * 2),
+            o(size_t(Hq) * P * D * 2);
+        auto hq = fill_normal(q, 900 + l), hk = fill_normal(k, 910 + l), hv = fill_normal(v, 920 + l);
+        Tensor Q = make_tensor(q.p, {1, Hq, P, D}), K = make_tensor(k.p, {1, Hkv, P, D}),
+               V = make_tensor(v.p, {1, Hkv, P, D}), out = make_tensor(o.p, {1, Hq, P, D});
+        out.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+        out.layer_id = l;
+        out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
+        out.op_params = {float(D), scale, 1.0f, float(G)};
+        ASSERT(kernel::dispatch(&out, 0), "prompt");
+        std::vector<uint16_t> want(size_t(Hq) * P * D);
+        or_paged_attention(ref, l, hq.data(), hk.data(), hv.data(), want.data(), 1, Hq, P, D, Hkv, G, scale, 1);
+    }
+    ASSERT(hipStreamSynchronize(s) == hipSuccess, "prompt done");
+    std::vector<float> hcos(size_t(max_seq) * D), hsin(size_t(max_seq) * D);
+    or_rope_cache(hcos.data(), 1e6f, D, max_seq, 1);
+    or_rope_cache(hsin.data(), 1e6f, D, max_seq, 0);
+    DevBuf dcos(hcos.size() * 4), dsin(hsin.size() * 4);
+    to_device(dcos.p, hcos);
+    to_device(dsin.p, hsin);
+    Tensor cos_t = make_tensor(dcos.p, {max_seq, D, 0, 0}, DataType::GGML_TYPE_F32),
+           sin_t = make_tensor(dsin.p, {max_seq, D, 0, 0}, DataType::GGML_TYPE_F32);
+    // fixed step buffers and nodes per layer
+    struct Layer {
+        std::unique_ptr<DevBuf> q, k, v, qr, kr, o;
+        Tensor xq, xk, rq, rk, vv, attn;
+    };
+    std::vector<Layer> ly(L);
+    for (int l = 0; l < L; ++l) {
+        Layer& y = ly[l];
+        y.q = std::make_unique<DevBuf>(size_t(Hq) * D * 2);
+        y.qr = std::make_unique<DevBuf>(size_t(Hq) * D * 2);
+        y.o = std::make_unique<DevBuf>(size_t(Hq) * D * 2);
+        y.k = std::make_unique<DevBuf>(size_t(Hkv) * D * 2);
+        y.kr = std::make_unique<DevBuf>(size_t(Hkv) * D * 2);
+        y.v = std::make_unique<DevBuf>(size_t(Hkv) * D * 2);
+        y.xq = make_tensor(y.q->p, {1, Hq, 1, D});
+        y.xk = make_tensor(y.k->p, {1, Hkv, 1, D});
+        y.vv = make_tensor(y.v->p, {1, Hkv, 1, D});
+        for (auto [r, x, buf, H] : {std::tuple{&y.rq, &y.xq, y.qr.get(), Hq}, std::tuple{&y.rk, &y.xk, y.kr.get(), Hkv}}) {
+            *r = make_tensor(buf->p, {1, H, 1, D});
+            r->op_type = OperationType::OP_TYPE_APPLY_ROPE;
+            r->src = {x, &cos_t, &sin_t, nullptr, nullptr, nullptr};
+            r->op_params = {float(D), float(D), 0.0f, 0};  // start_pos stale: the device position rules
+            r->layer_id = l;
+        }
+        y.attn = make_tensor(y.o->p, {1, Hq, 1, D});
+        y.attn.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+        y.attn.layer_id = l;
+        y.attn.src = {&y.rq, &y.rk, &y.vv, nullptr, nullptr, nullptr};
+        y.attn.op_params = {float(D), scale, 1.0f, float(G)};
+        pam.stage_decode(l, steps);
+    }
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    ASSERT(hipStreamBeginCapture(s, hipStreamCaptureModeGlobal) == hipSuccess, "begin capture");
+    for (int l = 0; l < L; ++l)
+        for (Tensor* t : {&ly[l].rq, &ly[l].rk, &ly[l].attn}) kernel::dispatch(t, 0);
+    ASSERT(hipStreamEndCapture(s, &g) == hipSuccess, "end capture");
+    ASSERT(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess, "instantiate");
+    for (int step = 0; step < steps && ok; ++step) {
+        const int32_t pos = P + step;
+        std::vector<std::vector<uint16_t>> hq(L), hk(L), hv(L);
+        for (int l = 0; l < L; ++l) {
+            hq[l] = fill_normal(*ly[l].q, 5000 + 10 * step + l);
+            hk[l] = fill_normal(*ly[l].k, 6000 + 10 * step + l);
+            hv[l] = fill_normal(*ly[l].v, 7000 + 10 * step + l);
+        }
+        ASSERT(hipGraphLaunch(ge, s) == hipSuccess, "replay");
+        ASSERT(hipStreamSynchronize(s) == hipSuccess, "replay done");
+        for (int l = 0; l < L && ok; ++l) {
+            std::vector<uint16_t> qr(size_t(Hq) * D), kr(size_t(Hkv) * D), want(size_t(Hq) * D);
+            or_apply_rope(qr.data(), hq[l].data(), hcos.data(), hsin.data(), Hq, 1, D, pos);
+            or_apply_rope(kr.data(), hk[l].data(), hcos.data(), hsin.data(), Hkv, 1, D, pos);
+            ASSERT(to_host<uint16_t>(ly[l].qr->p, qr.size()) == qr, "RoPE'd q at the device position bit-exact");
+            or_paged_attention(ref, l, qr.data(), kr.data(), hv[l].data(), want.data(), 1, Hq, 1, D, Hkv, G, scale, 1);
+            char what[80];
+            std::snprintf(what, sizeof what, "replay %d layer %d position %d", step, l, pos);
+            ok = attn_close(to_host<uint16_t>(ly[l].o->p, want.size()), want, what);
+        }
+    }
+    for (int l = 0; l < L && ok; ++l) {
+        ASSERT(pam.sync_decode(l) == P + steps && !pam.is_staged(l), "num_cached after sync");
+        const auto st = pam.get_layer(l);
+        std::vector<int32_t> rk(st.page_table.size()), rv(st.page_table.size());
+        ASSERT(or_mgr_get_page_table(ref, l, rk.data(), rv.data(), int32_t(rk.size())) == int32_t(rk.size()),
+               "page table length");
+        for (size_t i = 0; i < rk.size(); ++i)
+            ASSERT(st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
+        ASSERT(st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
+    }
+    (void)hipGraphExecDestroy(ge);
+    (void)hipGraphDestroy(g);
+    mm.set_stream(Device::HIP, 0, nullptr);
+    (void)hipStreamDestroy(s);
+    or_mgr_destroy(ref);
+    return ok;
+}
+
 bool test_paged_attention_qwen06b() { return run_paged_graph(16, 8, 40, 3, 0x5EED0001); }
 bool test_paged_attention_qwen4b() { return run_paged_graph(32, 8, 33, 3, 0x5EED0003); }
 
@@ -446,6 +582,7 @@ int main() {
         {"paged attention graph Qwen3-0.6B shape", test_paged_attention_qwen06b},
         {"paged attention graph Qwen3-4B shape", test_paged_attention_qwen4b},
         {"paged attention errors", test_paged_attention_errors},
+        {"decode step graph (device position)", test_decode_step_graph},
         {"flash attention causal", test_flash_attention_causal},
         {"flash attention full", test_flash_attention_full},
         {"flash attention one token", test_flash_attention_one_token},
