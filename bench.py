@@ -419,13 +419,39 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
         all_layers(0)
     g_us = time_kernels(torch, lambda i: graph.replay(), iters, warm=2)
     del graph
+    # The decode loop itself: one step (append this token's K/V, attend) of all
+    # 36 layers captured once at the device position and replayed token after
+    # token (genllm_kv_stage_decode / genllm_paged_attention_step / sync).
+    kn = torch.empty((layers, 1, Hkv, 1, D), dtype=torch.bfloat16, device="cuda")
+    vn = torch.empty_like(kn)
+    paged.fill_normal_bf16(kn, seed + 1)
+    paged.fill_normal_bf16(vn, seed + 2)
+    n_steps = iters + 2
+    for l in range(layers):
+        m5.stage_decode(l, n_steps)
+    torch.cuda.synchronize()
+    o5s = o5.unsqueeze(0)
+    step_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(step_graph):
+        for l in range(layers):
+            paged.paged_attention_step(m5, l, q5[l].unsqueeze(0), kn[l], vn[l], o5s, Hq // Hkv, 1.0 / np.sqrt(D))
+    s_us = time_kernels(torch, lambda i: step_graph.replay(), iters, warm=2)
+    for l in range(layers):
+        if m5.sync_decode(l) != N + n_steps:
+            raise RuntimeError("captured decode loop: device position did not advance once per replay")
+    del step_graph
     m5.close()
     b5 = layers * decode_kernel_bytes(N)
     gbs = b5 / (avg_us * 1e-6) / 1e9
+    s_bytes = sum(layers * decode_step_bytes(N + 1 + i) for i in range(2, n_steps)) / iters
     return {"total_us": round(avg_us, 2), "us_per_layer": round(avg_us / layers, 3), "bytes": b5,
             "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "graph_total_us": round(g_us, 2), "graph_us_per_layer": round(g_us / layers, 3),
-            "graph_GB_s": round(b5 / (g_us * 1e-6) / 1e9, 1)}
+            "graph_GB_s": round(b5 / (g_us * 1e-6) / 1e9, 1),
+            "decode_loop_graph": {"us_per_token": round(s_us, 2), "us_per_layer": round(s_us / layers, 3),
+                                  "GB_s": round(s_bytes / (s_us * 1e-6) / 1e9, 1), "tokens": iters,
+                                  "note": "36-layer append + attend step captured once at the device position "
+                                          "and replayed per token (position advanced on the GPU)"}}
 
 
 def linear_qkv(np, torch, paged, synth, call, iters=40):

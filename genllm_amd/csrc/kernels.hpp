@@ -85,7 +85,8 @@ struct AttnParams {
     // pages = ceil(n_cached / 16) -- instead of n_cached / new_from / n_pages,
     // which then only size the plan (n_pages = the most pages a step may
     // span).  A step past `limit` (or past n_pages) sets `error` and does
-    // nothing; otherwise the last workgroup to finish advances pos by S.
+    // nothing; otherwise the merge kernel advances pos by S (without one, the
+    // last split workgroup to finish does).
     int32_t* step = nullptr;
     // fused append (decode of the op): tokens at positions >= new_from are read
     // from k_new / v_new ([Hkv][S][D], strides in elements) instead of the

@@ -226,6 +226,44 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     const int h = blockIdx.x, sp = blockIdx.y;
     const int rows_total = p.G * p.S;  // <= 16
 
+    // q rows and the block-table entries of the wave's planned page range are
+    // requested first: neither depends on the cache position, so in a
+    // device-position step their round trip overlaps the position's.  (The
+    // table holds ids up to the planned end; the wave uses only those below
+    // the step's own end.)
+    const int r = n16;  // this lane's row (MFMA column): q head h*G + r%G, query r/G
+    const bool row_ok = r < rows_total;
+    bf16x8_t qb[KS];
+    {
+        const uint16_t* qrow = p.q + int64_t(h * p.G + r % p.G) * p.q_head_stride + int64_t(r / p.G) * p.q_tok_stride;
+#pragma unroll
+        for (int c = 0; c < KS; ++c) {
+            uint4 u = make_uint4(0, 0, 0, 0);
+            if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g);
+            qb[c] = as_bf16x8(u);
+        }
+    }
+    const int begin = sp * p.pages_per_split;
+    const int end_plan = min(begin + p.pages_per_split, p.n_pages);
+    const int np_plan = end_plan - begin - wv > 0 ? (end_plan - begin - wv + W - 1) / W : 0;
+    // fused append: page ids opened by this call come from the launch arguments
+    if (sp == 0 && h == 0 && threadIdx.x < p.upd.count) {
+        p.k_ids_w[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
+        p.v_ids_w[p.upd.first + threadIdx.x] = p.upd.v[threadIdx.x];
+    }
+    int my_kid = 0, my_vid = 0;  // block-table entries of the wave's pages, one per lane
+    if (lane < np_plan) {
+        const int pg = begin + wv + W * lane;
+        const int rel = pg - p.upd.first;
+        if (rel >= 0 && rel < p.upd.count) {
+            my_kid = p.upd.k[rel];
+            my_vid = p.upd.v[rel];
+        } else {
+            my_kid = p.k_ids[pg];
+            my_vid = p.v_ids[pg];
+        }
+    }
+
     // Cache position: from the launch arguments, or (device-position step)
     // from the control block, where a step that would pass the staged limit
     // or the pages the grid was planned for only raises the error flag.
@@ -244,41 +282,9 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         new_from = step_pos;
     }
 
-    // this lane's row (MFMA column): q head h*G + r%G, query r/G
-    const int r = n16;
-    const bool row_ok = r < rows_total;
     const int qabs = p.causal ? n_cached - p.S + r / p.G : n_cached - 1;
-    bf16x8_t qb[KS];
-    {
-        const uint16_t* qrow = p.q + int64_t(h * p.G + r % p.G) * p.q_head_stride + int64_t(r / p.G) * p.q_tok_stride;
-#pragma unroll
-        for (int c = 0; c < KS; ++c) {
-            uint4 u = make_uint4(0, 0, 0, 0);
-            if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g);
-            qb[c] = as_bf16x8(u);
-        }
-    }
-
-    const int begin = sp * p.pages_per_split;
     const int end = min(begin + p.pages_per_split, n_pages);
-    const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;
-    // fused append: page ids opened by this call come from the launch arguments
-    if (sp == 0 && h == 0 && threadIdx.x < p.upd.count) {
-        p.k_ids_w[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
-        p.v_ids_w[p.upd.first + threadIdx.x] = p.upd.v[threadIdx.x];
-    }
-    int my_kid = 0, my_vid = 0;  // block-table entries of the wave's pages, one per lane
-    if (lane < np) {
-        const int pg = begin + wv + W * lane;
-        const int rel = pg - p.upd.first;
-        if (rel >= 0 && rel < p.upd.count) {
-            my_kid = p.upd.k[rel];
-            my_vid = p.upd.v[rel];
-        } else {
-            my_kid = p.k_ids[pg];
-            my_vid = p.v_ids[pg];
-        }
-    }
+    const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;  // <= np_plan
     // Element offsets inside a page (< 2^31): lane's K operand chunk (token
     // n16, dims 8g + 32c) and V row chunk (token 4g + i, dims 8 n16).  Page
     // bases are wave-uniform, so a load is a scalar base plus this offset.
@@ -528,10 +534,12 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         }
     }
     if constexpr (kStep) {
-        // Every workgroup read the position before it counts here, so the
-        // last to arrive may advance it (and re-arm the counter) for the next
-        // step.  The kernel boundary publishes both to the next launch.
-        if (threadIdx.x == 0) {
+        // Without a merge kernel (one split, or the single-launch merge) the
+        // last workgroup to arrive advances the position: every workgroup
+        // read it before it counts here.  The kernel boundary publishes the
+        // position and the re-armed counter to the next launch.  With a merge
+        // kernel, that kernel advances it.
+        if (threadIdx.x == 0 && (p.n_splits == 1 || p.counters)) {
             const int total = int(gridDim.x * gridDim.y);
             const int old =
                 __hip_atomic_fetch_add(p.step + kStepArrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -567,8 +575,14 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
     __shared__ float s_m[MW], s_l[MW];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int h = blockIdx.x, ri = blockIdx.y, d0 = kMergeDims * int(blockIdx.z);
-    // device-position step refused by the split kernel: no partials to merge
-    if (p.step && step_load(p.step + kStepError)) return;
+    if (p.step) {
+        // device-position step refused by the split kernel: no partials to merge
+        if (step_load(p.step + kStepError)) return;
+        // every split workgroup has read the position (they ran before this
+        // launch): advance it for the next step, without waiting for the result
+        if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0)
+            __hip_atomic_fetch_add(p.step + kStepPos, p.S, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const int rows = p.G * p.S;
     const int ns = p.n_splits;  // <= kMaxSplits
     const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
