@@ -577,10 +577,19 @@ def measure_counters():
                       round(statistics.mean(e - b for b, e in v) / 1e3, 3) for k, v in timed.items()}
         t0 = min(v[0][0] for v in timed.values())
         t1 = max(v[-1][1] for v in timed.values())
+        # the traced process also timed the same launches with HIP events
+        ev = None
+        with open(os.path.join(tmp, "kernel_trace.log")) as log:
+            for line in log:
+                if line.startswith("{") and "events_us_per_launch" in line:
+                    ev = json.loads(line)["events_us_per_launch"]
         res["kernel_trace"] = {"mean_us": per_kernel, "sum_us": round(sum(per_kernel.values()), 3),
                                "timeline_us_per_decode": round((t1 - t0) / 1e3 / n, 3), "decodes": n,
-                               "note": "durations under rocprofv3 --kernel-trace, which itself adds about "
-                                       "0.6 us per dispatch against the event-timed avg_launch_us"}
+                               "events_us_per_decode_traced": ev,
+                               "note": "durations under rocprofv3 --kernel-trace; events_us_per_decode_traced is "
+                                       "the same launches timed with HIP events inside the traced process, so "
+                                       "(events_us_per_decode_traced - avg_launch_us) is what the profiler adds "
+                                       "per decode (two dispatches)"}
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     res["bytes"] = res["FETCH_SIZE"]["bytes"] + res["WRITE_SIZE"]["bytes"]
