@@ -247,3 +247,64 @@ def test_step_head_dim_256_across_8192(orc):
     assert st.mgr.sync_decode(0) == P + 12
     st.check_host_state("after sync")
     st.close()
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,P,rope_dim,merge", [
+    (16, 8, 128, 2, 40, 128, None),     # two tokens per step (append_tokens), pages opened at 48 and 64
+    (32, 8, 128, 1, 5, 128, None),      # one split: the last split workgroup advances the position
+    (32, 8, 128, 1, 200, 128, "fused"),  # single-launch merge: no merge kernel either
+    (8, 2, 256, 1, 90, 64, None),       # Qwen3.5: RoPE on the first 64 of 256 dims
+])
+def test_step_variants(orc, monkeypatch, Hq, Hkv, D, S, P, rope_dim, merge):
+    """Device-position steps beyond the single-token default plan: the query
+    chunk, the split plan, the merge form and the rotary width change, and
+    every replay still matches the oracle run with host positions (RoPE'd q
+    bit-exact, attention within tolerance, pools bit-exact)."""
+    if merge:
+        monkeypatch.setenv("GENLLM_DECODE_MERGE", merge)
+    G, L, steps, max_seq = Hq // Hkv, 2, 8, 512
+    pool = (P + S * steps + 15) // 16 + 2
+    st = Stack(orc, L, Hq, Hkv, D, pool=pool, P=P, seed=0x5EED0400 + S + D + P)
+    dev = dict(dtype=torch.bfloat16, device="cuda")
+    q_raw = torch.zeros((L, Hq, S, D), **dev)
+    k_raw = torch.zeros((L, Hkv, S, D), **dev)
+    v_in = torch.zeros((L, 1, Hkv, S, D), **dev)
+    q_rot = torch.zeros((L, 1, Hq, S, D), **dev)
+    k_rot = torch.zeros((L, 1, Hkv, S, D), **dev)
+    out = torch.zeros((L, 1, Hq, S, D), **dev)
+    cos, sin = orc.rope_cache(THETA, rope_dim, max_seq)
+    cos_t, sin_t = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    rope = orc.apply_rope if rope_dim == D else orc.apply_rope_partial
+    for l in range(L):
+        st.mgr.stage_decode(l, S * steps)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for l in range(L):
+            paged.apply_rope_step(st.mgr, l, q_rot[l, 0], q_raw[l], cos_t, sin_t)
+            paged.apply_rope_step(st.mgr, l, k_rot[l, 0], k_raw[l], cos_t, sin_t)
+            paged.paged_attention_step(st.mgr, l, q_rot[l], k_rot[l], v_in[l], out[l], G, scale_for(D))
+    for i in range(steps):
+        pos = P + S * i
+        print(f"replay {i}: positions {pos}..{pos + S - 1}", flush=True)
+        q = synth.normal_bf16(11000 + 10 * i, (L, Hq, S, D))
+        k = synth.normal_bf16(11001 + 10 * i, (L, Hkv, S, D))
+        v = synth.normal_bf16(11002 + 10 * i, (L, 1, Hkv, S, D))
+        q_raw.copy_(paged.to_device_bf16(q))
+        k_raw.copy_(paged.to_device_bf16(k))
+        v_in.copy_(paged.to_device_bf16(v))
+        out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        got, got_q = bits(out), bits(q_rot)
+        for l in range(L):
+            qr, kr = rope(q[l], cos, sin, pos), rope(k[l], cos, sin, pos)
+            assert np.array_equal(got_q[l, 0], qr), f"replay {i} layer {l}: RoPE'd q"
+            want, rc = st.ref.paged_attention(l, qr[None], kr[None], v[l], G, scale_for(D))
+            assert rc == 0
+            assert_attn_close(got[l], want, f"replay {i} layer {l} positions {pos}..")
+        st.check_pools(f"replay {i}")
+    for l in range(L):
+        assert st.mgr.sync_decode(l) == P + S * steps
+    st.check_host_state("after sync")
+    st.close()
