@@ -85,15 +85,20 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(const bf16x8_t& a, const bf16x8
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Two fp32 -> packed bf16 for an output: round to nearest even, an fp32
-// subnormal becomes a signed zero -- bfloat16_t's constructor
-// (bfloat16.hpp:18-41) for every finite value -- in three instructions
-// (v_cvt_pk_bf16_f32 and two flushes) instead of the integer form's
-// branches; a NaN stays a (quiet) NaN.
+// Two fp32 -> packed bf16 for an output, bfloat16_t's constructor
+// (bfloat16.hpp:18-41) for every input: round to nearest even, an fp32
+// subnormal becomes a signed zero, a NaN becomes sign | 0x7F81 (the
+// constructor keeps only "mantissa != 0") -- v_cvt_pk_bf16_f32 plus selects
+// instead of the integer form's branches.
 __device__ __forceinline__ uint32_t bf16_pair_out(float lo, float hi) {
+    const uint32_t nan_lo = ((__float_as_uint(lo) >> 16) & 0x8000u) | 0x7F81u;
+    const uint32_t nan_hi = (__float_as_uint(hi) & 0x80000000u) | 0x7F810000u;
+    const bool lo_nan = lo != lo, hi_nan = hi != hi;
     lo = fabsf(lo) < __FLT_MIN__ ? __builtin_copysignf(0.0f, lo) : lo;
     hi = fabsf(hi) < __FLT_MIN__ ? __builtin_copysignf(0.0f, hi) : hi;
-    return bf16_pair_rne(lo, hi);
+    uint32_t r = bf16_pair_rne(lo, hi);
+    r = lo_nan ? (r & 0xFFFF0000u) | nan_lo : r;
+    return hi_nan ? (r & 0xFFFFu) | nan_hi : r;
 }
 
 // s_waitcnt operand: vmcnt(n) for n < 16, other counters unconstrained
