@@ -11,6 +11,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <set>
 #include <vector>
 
@@ -54,8 +55,7 @@ public:
     PagedAttentionManager(const PagedAttentionManager&) = delete;
     PagedAttentionManager& operator=(const PagedAttentionManager&) = delete;
 
-    // page_attention.h:57-66.  get_layer returns a snapshot; the table is
-    // changed through set_page_table (the reference mutates it in place).
+    // page_attention.h:57-66
     struct LayerState {
         bool active = false;
         int32_t num_cached = 0;
@@ -67,7 +67,18 @@ public:
         std::vector<PageEntry> page_table;
     };
 
-    [[nodiscard]] LayerState get_layer(int32_t layer_id) const;
+    // page_attention.h:68.  The reference hands out a reference into its layer
+    // map that later calls keep current (test_page_attention.cpp:53-61 reads
+    // num_cached and page_table through it after append_kv_pages).  The state
+    // lives in the native manager here, so get_layer returns a view that this
+    // manager refreshes after each of its own calls and after each PAGED_ATTN
+    // node run on it; the view is const, and the table is changed through
+    // set_page_table.  A native call made around this manager (genllm_kv_*
+    // on handle()) shows in the view at its next refresh_layer or get_layer.
+    [[nodiscard]] const LayerState& get_layer(int32_t layer_id);
+    // Re-reads layer_id's view, if get_layer has handed one out (a no-op
+    // otherwise, so the decode path pays nothing while nobody holds a view).
+    void refresh_layer(int32_t layer_id);
     void set_page_table(int32_t layer_id, const std::vector<PageEntry>& table, int32_t num_cached);
 
     void reserve_layer(int32_t layer_id, int32_t max_blocks);                                      // :81-101
@@ -104,6 +115,9 @@ private:
     int32_t device_ = 0;
     void* stream_ = nullptr;
     std::set<int32_t> staged_;
+    std::map<int32_t, LayerState> views_;  // node-stable: get_layer's references stay valid
+    void read_layer(int32_t layer_id, LayerState& s) const;
+    void refresh_views();
 };
 
 // Throws std::runtime_error carrying genllm_last_error() when status != 0.

@@ -57,6 +57,7 @@ void PagedAttentionImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     genllm_check(entry(mgr->handle(), layer_id, Q->data, K->data, V->data, out->data, batch, num_q_heads, seq_len,
                        head_dim, num_kv_heads, num_kv_groups, scale, causal ? 1 : 0, mgr->stream()),
                  "paged_attention");
+    mgr->refresh_layer(layer_id);  // the op appended the chunk: keep get_layer's view current
 }
 
 // src/backend/cpu/attention.cpp:39-121

@@ -12,6 +12,21 @@ void genllm_check(int status, const char* what) {
     if (status != GENLLM_OK) throw std::runtime_error(std::string(what) + ": " + genllm_last_error());
 }
 
+namespace {
+// Refreshes a layer's get_layer view when a manager call ends, also when it
+// throws after a partial change (a scatter failing after its pages opened).
+struct ViewRefresh {
+    PagedAttentionManager& mgr;
+    int32_t layer;
+    ~ViewRefresh() {
+        try {
+            mgr.refresh_layer(layer);
+        } catch (...) {  // the call's own error is the one that propagates
+        }
+    }
+};
+}  // namespace
+
 // ------------------------------------------------------------- BlockPool
 int32_t BlockPool::alloc() {
     int32_t id = -1;
@@ -53,10 +68,9 @@ PagedAttentionManager::~PagedAttentionManager() {
     if (kv_) genllm_kv_destroy(kv_);
 }
 
-PagedAttentionManager::LayerState PagedAttentionManager::get_layer(int32_t layer_id) const {
+void PagedAttentionManager::read_layer(int32_t layer_id, LayerState& s) const {
     genllm_layer_info info;
     genllm_check(genllm_kv_layer_info(kv_, layer_id, &info), "get_layer");
-    LayerState s;
     s.active = info.active != 0;
     s.num_cached = info.num_cached;
     s.n_kv_heads = info.n_kv_heads;
@@ -69,11 +83,28 @@ PagedAttentionManager::LayerState PagedAttentionManager::get_layer(int32_t layer
     genllm_check(genllm_kv_page_table(kv_, layer_id, k.data(), v.data(), info.num_pages, &n), "get_layer");
     s.page_table.resize(size_t(n));
     for (int32_t i = 0; i < n; ++i) s.page_table[size_t(i)] = PageEntry{k[size_t(i)], v[size_t(i)]};
-    return s;
+}
+
+const PagedAttentionManager::LayerState& PagedAttentionManager::get_layer(int32_t layer_id) {
+    LayerState s;
+    read_layer(layer_id, s);  // throws for an unknown layer before a view exists
+    LayerState& view = views_[layer_id];
+    view = std::move(s);
+    return view;
+}
+
+void PagedAttentionManager::refresh_layer(int32_t layer_id) {
+    auto it = views_.find(layer_id);
+    if (it != views_.end()) read_layer(layer_id, it->second);
+}
+
+void PagedAttentionManager::refresh_views() {
+    for (auto& [id, view] : views_) read_layer(id, view);
 }
 
 void PagedAttentionManager::set_page_table(int32_t layer_id, const std::vector<PageEntry>& table,
                                            int32_t num_cached) {
+    ViewRefresh refresh{*this, layer_id};
     std::vector<int32_t> k(table.size()), v(table.size());
     for (size_t i = 0; i < table.size(); ++i) {
         k[i] = table[i].k_block_id;
@@ -85,16 +116,19 @@ void PagedAttentionManager::set_page_table(int32_t layer_id, const std::vector<P
 }
 
 void PagedAttentionManager::reserve_layer(int32_t layer_id, int32_t max_blocks) {
+    ViewRefresh refresh{*this, layer_id};
     genllm_check(genllm_kv_reserve_layer(kv_, layer_id, max_blocks), "reserve_layer");
 }
 
 void PagedAttentionManager::init_layer(int32_t layer_id, int32_t n_kv_heads, int32_t head_dim, DataType dtype) {
+    ViewRefresh refresh{*this, layer_id};
     genllm_check(genllm_kv_init_layer(kv_, layer_id, n_kv_heads, head_dim, int32_t(dtype)), "init_layer");
 }
 
 void PagedAttentionManager::append_kv_from_tensor(int32_t layer_id, const void* K_data, const void* V_data,
                                                   int32_t n_kv_heads, int32_t seq_len, int32_t head_dim,
                                                   DataType dtype) {
+    ViewRefresh refresh{*this, layer_id};
     genllm_layer_info info;
     genllm_check(genllm_kv_layer_info(kv_, layer_id, &info), "append_kv_from_tensor");
     if (!info.active || seq_len <= 0) return;  // page_attention.cpp:106-107
@@ -113,26 +147,31 @@ void PagedAttentionManager::append_kv_from_tensor(int32_t layer_id, const void* 
 void PagedAttentionManager::append_kv_from_pos(int32_t layer_id, const void* K_data, const void* V_data,
                                                int32_t n_kv_heads, int32_t head_dim, DataType dtype,
                                                int32_t global_pos, int32_t count) {
+    ViewRefresh refresh{*this, layer_id};
     genllm_check(genllm_kv_append_from_pos(kv_, layer_id, K_data, V_data, n_kv_heads, head_dim, int32_t(dtype),
                                            global_pos, count, stream_),
                  "append_kv_from_pos");
 }
 
 void PagedAttentionManager::append_kv_pages(int32_t layer_id, int32_t count) {
+    ViewRefresh refresh{*this, layer_id};
     genllm_check(genllm_kv_append_pages(kv_, layer_id, count, stream_), "append_kv_pages");
 }
 
 void PagedAttentionManager::reset() {
     genllm_check(genllm_kv_reset(kv_), "reset");
     staged_.clear();  // the native reset leaves every layer host-driven
+    refresh_views();
 }
 
 void PagedAttentionManager::stage_decode(int32_t layer_id, int32_t n_tokens) {
+    ViewRefresh refresh{*this, layer_id};
     genllm_check(genllm_kv_stage_decode(kv_, layer_id, n_tokens, stream_), "stage_decode");
     staged_.insert(layer_id);
 }
 
 int32_t PagedAttentionManager::sync_decode(int32_t layer_id) {
+    ViewRefresh refresh{*this, layer_id};
     int32_t n = 0;
     const int rc = genllm_kv_sync_decode(kv_, layer_id, stream_, &n);
     staged_.erase(layer_id);  // synced even when it reports a refused step

@@ -147,13 +147,18 @@ bool test_block_pool_reset() {
 bool test_page_table_append_kv() {
     PagedAttentionManager mgr(0, 1 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
-    ASSERT(mgr.get_layer(0).active, "layer active");
-    ASSERT(mgr.get_layer(0).num_cached == 0, "initially 0 cached");
+    // held across the appends, as test_page_attention.cpp:53-61 holds it
+    auto& layer = mgr.get_layer(0);
+    ASSERT(layer.active, "layer active");
+    ASSERT(layer.num_cached == 0, "initially 0 cached");
     mgr.append_kv_pages(0, 1);
-    ASSERT(mgr.get_layer(0).num_cached == 1, "1 token cached");
+    ASSERT(layer.num_cached == 1, "1 token cached");
     mgr.append_kv_pages(0, 31);
-    ASSERT(mgr.get_layer(0).num_cached == 32, "32 tokens cached");
-    ASSERT(mgr.get_layer(0).page_table.size() == 2, "2 pages (16+16)");
+    ASSERT(layer.num_cached == 32, "32 tokens cached");
+    ASSERT(layer.page_table.size() == 2, "2 pages (16+16)");
+    ASSERT(&mgr.get_layer(0) == &layer, "one view per layer");
+    mgr.reset();
+    ASSERT(layer.num_cached == 0 && layer.page_table.empty(), "reset shows in the view");
     return true;
 }
 
@@ -222,6 +227,7 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
         or_mgr_reserve_layer(ref, l, (max_seq + 15) / 16);
     }
     bool ok = true;
+    const auto& live = pam.get_layer(L - 1);  // kept current by the PAGED_ATTN nodes themselves
     for (int step = 0; step <= steps && ok; ++step) {
         const int32_t S = step == 0 ? s0 : 1;
         for (int l = 0; l < L && ok; ++l) {
@@ -250,6 +256,7 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
             for (int32_t i = 0; i < n; ++i)
                 ASSERT(st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
             ASSERT(st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
+            ASSERT(live.num_cached == or_mgr_num_cached(ref, L - 1), "held view follows the op");
         }
     }
     for (int l = 0; l < L && ok; ++l) {
