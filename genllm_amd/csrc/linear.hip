@@ -5,9 +5,10 @@
 // x [rows][common], w [cols][common] (transpose_w = 1), bias [cols] or null,
 // fp32 accumulation, one rounding (the bfloat16_t constructor's rules).
 //
-// rows <= kGemvRows (a decode step): linear_gemv_kernel, HBM-bound on the
-// weights, reproduces the CPU reference's summation order exactly, so the
-// result is bit-identical to it.  The reference sums each output over K-blocks
+// rows <= kGemvRows (a decode step): linear_gemv_lds_kernel when every K-block
+// is whole, else linear_gemv_kernel; both HBM-bound on the weights, both
+// reproduce the CPU reference's summation order exactly, so the result is
+// bit-identical to it.  The reference sums each output over K-blocks
 // of 256 elements: inside a block two 8-lane accumulators (sum0 takes elements
 // 16i+l, sum1 elements 16i+8+l, one fused multiply-add each, i ascending), then
 // v = sum0 + sum1 lane-wise and the block adds (t0+t1)+(t2+t3), t[i] =
@@ -41,6 +42,9 @@ namespace {
 constexpr int kGemvRows = 4;     // rows handled by the order-exact kernel
 constexpr int kBlockK = 256;     // the reference's K blocking (KR)
 constexpr int kGemvThreads = 256;
+// dynamic LDS of linear_gemv_lds_kernel: the weight rows of a workgroup (at
+// most 64 KB) and the x rows; two workgroups still fit a CU (160 KB)
+constexpr size_t kGemvLdsMax = 80 * 1024;
 
 __device__ __forceinline__ void bf16x8_to_f32(const uint4& u, float f[8]) {
     f[0] = bf16_lo(u.x); f[1] = bf16_hi(u.x);
@@ -162,6 +166,110 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_kernel(const uint16_
     }
 }
 
+// The same sums when every K-block is whole (common % 256 == 0), with the
+// weight rows staged through LDS.  In linear_gemv_kernel a wave's 16-byte
+// weight loads touch 32 cache lines each (a lane reads 32 B of every 512-byte
+// block), and every lane also loads its 256 B of x: twice the weight bytes go
+// through the L1.  Here the workgroup's weight rows -- cpw whole columns, one
+// contiguous range -- come in with LDS-mode buffer loads of 1 KB per wave
+// instruction, x once per workgroup the same way, and each lane then reads its
+// block from LDS.  Block P of the workgroup (lane pair P: column P / nb, block
+// P % nb, as in linear_gemv_kernel) is stored rotated by 2P chunks of 16 B
+// (chunk q at position (q + 2P) % 32), x's block b by 2b, so that the 16 lanes
+// of a read phase hit 16 different bank groups.  The multiply-add order and the
+// block sums are those of linear_gemv_kernel.  Loads past the weights or x (the
+// last workgroup, an odd block count) are bounded by the buffer resources and
+// read zeros into LDS slots no lane reads.  (Measured against block-major slots,
+// whose read phases share x's block, and x staged as fp32: both slower.)
+template <int R>
+__global__ __launch_bounds__(kGemvThreads) void linear_gemv_lds_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ w,
+                                                                       const uint16_t* __restrict__ bias,
+                                                                       uint16_t* __restrict__ out, int common,
+                                                                       int cols, int nb, int cpw) {
+    extern __shared__ __attribute__((aligned(16))) char lds_w[];
+    __shared__ float s_h1[R][kGemvThreads / 2];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    constexpr int kWaves = kGemvThreads / 64;
+    const int col0 = int(blockIdx.x) * cpw;
+    const int n_pairs = cpw * nb;                 // 512-byte blocks of this workgroup
+    const int w_inst = (n_pairs + 1) / 2;         // 1 KB loads of them
+    const int x_inst = (nb + 1) / 2;              // 1 KB loads per row of x
+    const int x_base = w_inst * 1024;             // x rows after the weights
+    {
+        const int64_t left = int64_t(cols - col0) * common * 2;
+        const uint32_t span = uint32_t(min<int64_t>(left, int64_t(n_pairs) * 512));
+        const auto rw = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(w + int64_t(col0) * common), 0, span, kBufferFlags);
+        const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, uint32_t(R * common * 2),
+                                                          kBufferFlags);
+        const int half = lane >> 5, pos = lane & 31;  // block of the 1 KB, LDS chunk position in it
+        for (int e = wv; e < w_inst; e += kWaves) {
+            const int P = 2 * e + half;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(lds_w + e * 1024),
+                                                     16, uint32_t(P * 512 + ((pos - 2 * P) & 31) * 16), 0, 0, 0);
+        }
+        for (int e = wv; e < R * x_inst; e += kWaves) {
+            const int r = e / x_inst, bb = 2 * (e - r * x_inst) + half;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, (__attribute__((address_space(3))) void*)(lds_w + x_base + e * 1024), 16,
+                uint32_t(r * common * 2 + bb * 512 + ((pos - 2 * bb) & 31) * 16), 0, 0, 0);
+        }
+    }
+    const int pair = t >> 1, h = t & 1;
+    const int lc = pair / nb, b = pair - lc * nb;  // column within the workgroup, block
+    const bool item = pair < n_pairs && col0 + lc < cols;
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+
+    float s[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) s[r][l] = 0.0f;
+    if (item) {
+        const char* wl = lds_w + pair * 512;
+        const char* xl = lds_w + x_base + b * 512;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int q = 2 * i + h;
+            float wf[8];
+            bf16x8_to_f32(*reinterpret_cast<const uint4*>(wl + ((q + 2 * pair) & 31) * 16), wf);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float xf[8];
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(xl + r * x_inst * 1024 + ((q + 2 * b) & 31) * 16), xf);
+#pragma unroll
+                for (int l = 0; l < 8; ++l) s[r][l] = __builtin_fmaf(xf[l], wf[l], s[r][l]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float v[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const float o = __shfl_xor(s[r][l], 1);
+            v[l] = h == 0 ? s[r][l] + o : o + s[r][l];
+        }
+        if (h == 0) s_h1[r][pair] = tree8(v);
+    }
+    __syncthreads();
+    if (t < cpw && col0 + t < cols) {
+        const int cc = col0 + t;
+        const float bv = bias ? bf16_to_f32(bias[cc]) : 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float acc = 0.0f;
+            for (int bb = 0; bb < nb; ++bb) acc += s_h1[r][t * nb + bb];
+            float val = acc;
+            if (bias) val += bv;
+            out[int64_t(r) * cols + cc] = uint16_t(f32_to_bf16_ref(val));
+        }
+    }
+}
+
 // out = bf16(acc + bias) over the fp32 GEMM result [rows][cols]
 __global__ __launch_bounds__(256) void linear_epilogue_kernel(const float* __restrict__ acc,
                                                               const uint16_t* __restrict__ bias,
@@ -217,6 +325,17 @@ int launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, ui
         const int cpw = kGemvThreads / (2 * nb);
         const unsigned grid = unsigned((cols + cpw - 1) / cpw);
         const int c = int(common), n = int(cols);
+        const size_t lds = size_t((cpw * nb + 1) / 2) * 1024 + size_t(rows) * ((nb + 1) / 2) * 1024;
+        if (common % kBlockK == 0 && lds <= kGemvLdsMax) {
+            switch (rows) {
+                case 1: hipLaunchKernelGGL(linear_gemv_lds_kernel<1>, dim3(grid), dim3(kGemvThreads), lds, stream, x, w, bias, out, c, n, nb, cpw); break;
+                case 2: hipLaunchKernelGGL(linear_gemv_lds_kernel<2>, dim3(grid), dim3(kGemvThreads), lds, stream, x, w, bias, out, c, n, nb, cpw); break;
+                case 3: hipLaunchKernelGGL(linear_gemv_lds_kernel<3>, dim3(grid), dim3(kGemvThreads), lds, stream, x, w, bias, out, c, n, nb, cpw); break;
+                default: hipLaunchKernelGGL(linear_gemv_lds_kernel<4>, dim3(grid), dim3(kGemvThreads), lds, stream, x, w, bias, out, c, n, nb, cpw); break;
+            }
+            GENLLM_LAUNCH_CHECK("linear_gemv_lds_kernel");
+            return GENLLM_OK;
+        }
         switch (rows) {
             case 1: hipLaunchKernelGGL(linear_gemv_kernel<1>, dim3(grid), dim3(kGemvThreads), 0, stream, x, w, bias, out, c, n, nb, cpw); break;
             case 2: hipLaunchKernelGGL(linear_gemv_kernel<2>, dim3(grid), dim3(kGemvThreads), 0, stream, x, w, bias, out, c, n, nb, cpw); break;

@@ -47,6 +47,12 @@ def inputs(seed, rows, common, cols, wscale=0.05):
     (1, 8, 5),         # one 8-group only
     (4, 24, 1000),
     (1, 32768, 3),     # 128 K-blocks: one column per workgroup
+    # whole K-blocks: the LDS-staged kernel (weights and x through LDS)
+    (4, 2560, 6144),
+    (3, 512, 77),      # the last workgroup holds 13 of its 64 columns
+    (2, 1280, 101),    # 5 blocks per column: an odd block count per workgroup (125)
+    (1, 4096, 130),
+    (2, 8192, 64),     # 80 KB of LDS: the largest staged shape
 ])
 def test_linear_gemv_bit_exact(orc, rows, common, cols):
     x, w, b = inputs(rows * 1000 + common + cols, rows, common, cols)
