@@ -67,17 +67,22 @@ public:
         std::vector<PageEntry> page_table;
     };
 
-    // page_attention.h:68.  The reference hands out a reference into its layer
-    // map that later calls keep current (test_page_attention.cpp:53-61 reads
-    // num_cached and page_table through it after append_kv_pages).  The state
-    // lives in the native manager here, so get_layer returns a view that this
-    // manager refreshes after each of its own calls and after each PAGED_ATTN
-    // node run on it; the view is const, and the table is changed through
-    // set_page_table.  A native call made around this manager (genllm_kv_*
-    // on handle()) shows in the view at its next refresh_layer or get_layer.
-    [[nodiscard]] const LayerState& get_layer(int32_t layer_id);
-    // Re-reads layer_id's view, if get_layer has handed one out (a no-op
-    // otherwise, so the decode path pays nothing while nobody holds a view).
+    // page_attention.h:68.  The reference hands out a mutable reference into
+    // its layer map: later calls show through it (test_page_attention.cpp:53-61
+    // reads num_cached and page_table after append_kv_pages), and a caller may
+    // set page_table / num_cached in place.  The state lives in the native
+    // manager here, so get_layer returns a view that this manager keeps in step
+    // both ways: an edit of the view's page_table or num_cached is committed
+    // (genllm_kv_set_page_table, with its checks) before the next call of this
+    // manager or PAGED_ATTN node on that layer, and the view is re-read after
+    // each of them.  The other fields are read-only in effect.  A native call
+    // made around this manager (genllm_kv_* on handle()) shows in the view at
+    // its next refresh_layer or get_layer.
+    [[nodiscard]] LayerState& get_layer(int32_t layer_id);
+    // Commits edits of layer_id's view, then re-reads it; both are no-ops
+    // unless get_layer has handed out a view of that layer, so the decode path
+    // pays nothing while nobody holds one.
+    void commit_layer(int32_t layer_id);
     void refresh_layer(int32_t layer_id);
     void set_page_table(int32_t layer_id, const std::vector<PageEntry>& table, int32_t num_cached);
 
@@ -116,8 +121,14 @@ private:
     void* stream_ = nullptr;
     std::set<int32_t> staged_;
     std::map<int32_t, LayerState> views_;  // node-stable: get_layer's references stay valid
+    struct Synced {                        // the native state a view last matched
+        int32_t num_cached = 0;
+        std::vector<PageEntry> page_table;
+    };
+    std::map<int32_t, Synced> synced_;
     void read_layer(int32_t layer_id, LayerState& s) const;
     void refresh_views();
+    void set_table_native(int32_t layer_id, const std::vector<PageEntry>& table, int32_t num_cached);
 };
 
 // Throws std::runtime_error carrying genllm_last_error() when status != 0.

@@ -52,6 +52,7 @@ void PagedAttentionImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     const float scale = out->op_params[1];
     const bool causal = int32_t(out->op_params[2]) != 0;
 
+    mgr->commit_layer(layer_id);  // edits of a get_layer view (a no-op without one)
     // a staged layer (device-position decode) reads its position on the device
     auto* const entry = mgr->is_staged(layer_id) ? genllm_paged_attention_step : genllm_paged_attention;
     genllm_check(entry(mgr->handle(), layer_id, Q->data, K->data, V->data, out->data, batch, num_q_heads, seq_len,

@@ -13,11 +13,13 @@ void genllm_check(int status, const char* what) {
 }
 
 namespace {
-// Refreshes a layer's get_layer view when a manager call ends, also when it
+// A manager call on one layer: edits of the layer's get_layer view are
+// committed first, and the view is re-read when the call ends, also when it
 // throws after a partial change (a scatter failing after its pages opened).
 struct ViewRefresh {
     PagedAttentionManager& mgr;
     int32_t layer;
+    ViewRefresh(PagedAttentionManager& m, int32_t l) : mgr(m), layer(l) { mgr.commit_layer(layer); }
     ~ViewRefresh() {
         try {
             mgr.refresh_layer(layer);
@@ -25,6 +27,13 @@ struct ViewRefresh {
         }
     }
 };
+
+bool same_table(const std::vector<PageEntry>& a, const std::vector<PageEntry>& b) {
+    if (a.size() != b.size()) return false;
+    for (size_t i = 0; i < a.size(); ++i)
+        if (a[i].k_block_id != b[i].k_block_id || a[i].v_block_id != b[i].v_block_id) return false;
+    return true;
+}
 }  // namespace
 
 // ------------------------------------------------------------- BlockPool
@@ -85,26 +94,45 @@ void PagedAttentionManager::read_layer(int32_t layer_id, LayerState& s) const {
     for (int32_t i = 0; i < n; ++i) s.page_table[size_t(i)] = PageEntry{k[size_t(i)], v[size_t(i)]};
 }
 
-const PagedAttentionManager::LayerState& PagedAttentionManager::get_layer(int32_t layer_id) {
+PagedAttentionManager::LayerState& PagedAttentionManager::get_layer(int32_t layer_id) {
+    commit_layer(layer_id);
     LayerState s;
     read_layer(layer_id, s);  // throws for an unknown layer before a view exists
     LayerState& view = views_[layer_id];
     view = std::move(s);
+    synced_[layer_id] = Synced{view.num_cached, view.page_table};
     return view;
+}
+
+void PagedAttentionManager::commit_layer(int32_t layer_id) {
+    auto it = views_.find(layer_id);
+    if (it == views_.end()) return;
+    const LayerState& v = it->second;
+    Synced& was = synced_[layer_id];
+    if (v.num_cached == was.num_cached && same_table(v.page_table, was.page_table)) return;
+    set_table_native(layer_id, v.page_table, v.num_cached);
+    was = Synced{v.num_cached, v.page_table};
 }
 
 void PagedAttentionManager::refresh_layer(int32_t layer_id) {
     auto it = views_.find(layer_id);
-    if (it != views_.end()) read_layer(layer_id, it->second);
+    if (it == views_.end()) return;
+    read_layer(layer_id, it->second);
+    synced_[layer_id] = Synced{it->second.num_cached, it->second.page_table};
 }
 
 void PagedAttentionManager::refresh_views() {
-    for (auto& [id, view] : views_) read_layer(id, view);
+    for (auto& [id, view] : views_) refresh_layer(id);
 }
 
 void PagedAttentionManager::set_page_table(int32_t layer_id, const std::vector<PageEntry>& table,
                                            int32_t num_cached) {
     ViewRefresh refresh{*this, layer_id};
+    set_table_native(layer_id, table, num_cached);
+}
+
+void PagedAttentionManager::set_table_native(int32_t layer_id, const std::vector<PageEntry>& table,
+                                             int32_t num_cached) {
     std::vector<int32_t> k(table.size()), v(table.size());
     for (size_t i = 0; i < table.size(); ++i) {
         k[i] = table[i].k_block_id;
@@ -159,6 +187,7 @@ void PagedAttentionManager::append_kv_pages(int32_t layer_id, int32_t count) {
 }
 
 void PagedAttentionManager::reset() {
+    // pending view edits are dropped with the rest of the state (page_attention.cpp:208-216)
     genllm_check(genllm_kv_reset(kv_), "reset");
     staged_.clear();  // the native reset leaves every layer host-driven
     refresh_views();

@@ -162,6 +162,39 @@ bool test_page_table_append_kv() {
     return true;
 }
 
+// get_layer's reference is writable, as the reference's is: an in-place edit
+// of page_table reaches the native table before the next call on the layer.
+bool test_get_layer_edit_in_place() {
+    PagedAttentionManager mgr(0, 4 << 20);
+    mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
+    mgr.reserve_layer(0, 8);
+    auto& layer = mgr.get_layer(0);
+    mgr.append_kv_pages(0, 32);
+    ASSERT(layer.page_table.size() == 2, "2 pages");
+    const PageEntry p0 = layer.page_table[0], p1 = layer.page_table[1];
+    std::swap(layer.page_table[0], layer.page_table[1]);  // e.g. a permuted table, set in place
+    mgr.append_kv_pages(0, 1);                           // commits the edit, then opens page 2
+    ASSERT(layer.num_cached == 33 && layer.page_table.size() == 3, "append after the edit");
+    ASSERT(layer.page_table[0].k_block_id == p1.k_block_id && layer.page_table[1].k_block_id == p0.k_block_id,
+           "edit kept");
+    std::vector<int32_t> k(3), v(3);
+    int32_t n = 0;
+    ASSERT(genllm_kv_page_table(mgr.handle(), 0, k.data(), v.data(), 3, &n) == 0 && n == 3, "native table");
+    ASSERT(k[0] == p1.k_block_id && v[0] == p1.v_block_id && k[1] == p0.k_block_id, "native table holds the edit");
+    layer.page_table[0].k_block_id = 1000;  // not a block the pool handed out
+    bool threw = false;
+    try {
+        mgr.append_kv_pages(0, 1);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    ASSERT(threw, "an invalid edit is refused at commit");
+    layer.page_table[0].k_block_id = p1.k_block_id;
+    mgr.append_kv_pages(0, 1);
+    ASSERT(layer.num_cached == 34, "usable again once the edit is valid");
+    return true;
+}
+
 bool test_page_table_multi_layer() {
     PagedAttentionManager mgr(0, 1 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_F16);
@@ -585,6 +618,7 @@ int main() {
         {"block_pool reset", test_block_pool_reset},
         {"page_table append_kv", test_page_table_append_kv},
         {"page_table multi layer", test_page_table_multi_layer},
+        {"get_layer edit in place", test_get_layer_edit_in_place},
         {"kv_cache_per_layer switch + sizing", test_kv_cache_per_layer_switch},
         {"paged attention graph Qwen3-0.6B shape", test_paged_attention_qwen06b},
         {"paged attention graph Qwen3-4B shape", test_paged_attention_qwen4b},
