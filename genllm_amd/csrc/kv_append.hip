@@ -66,18 +66,30 @@ struct Append {
     // Both candidates are loaded from their own address space (launch
     // arguments, device table) and the value is selected: a pointer select
     // would make a flat load that waits on every outstanding access.
-    __device__ __forceinline__ static int32_t page_id(const AppendParams& p, int lp, int which) {
+    __device__ __forceinline__ static void page_id_loads(const AppendParams& p, int lp, int which, int32_t& from_args,
+                                                         int32_t& from_table) {
         const int rel = lp - p.upd.first;
         const bool opened = rel >= 0 && rel < p.upd.count;
-        const int32_t from_args = (which ? p.upd.v : p.upd.k)[opened ? rel : 0];
-        const int32_t from_table = (which ? p.v_ids : p.k_ids)[lp];
+        from_args = (which ? p.upd.v : p.upd.k)[opened ? rel : 0];
+        from_table = (which ? p.v_ids : p.k_ids)[lp];
+    }
+    __device__ __forceinline__ static int32_t page_id_pick(const AppendParams& p, int lp, int32_t from_args,
+                                                           int32_t from_table) {
+        const int rel = lp - p.upd.first;
+        const bool opened = rel >= 0 && rel < p.upd.count;
         const int32_t id = opened ? from_args : from_table;
         return (id >= 0 && id < p.max_blocks) ? id : -1;
     }
+    __device__ __forceinline__ static int32_t page_id(const AppendParams& p, int lp, int which) {
+        int32_t a, t;
+        page_id_loads(p, lp, which, a, t);
+        return page_id_pick(p, lp, a, t);
+    }
 
-    __device__ __forceinline__ static uint16_t* k_dst(const AppendParams& p, int tok, int h) {
+    __device__ __forceinline__ static uint16_t* k_dst(const AppendParams& p, int tok, int h, int32_t from_args,
+                                                      int32_t from_table) {
         const int gpos = p.pos0 + tok;
-        const int64_t id = page_id(p, gpos / kPage, 0);
+        const int64_t id = page_id_pick(p, gpos / kPage, from_args, from_table);
         if (id < 0) return nullptr;
         return p.k_pool + id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + h * D;
     }
@@ -159,7 +171,11 @@ struct Append {
         const int ngq = p.nq_tasks, ngk = p.nkv_tasks;
         const int64_t nq = int64_t(p.S) * ngq, nk = int64_t(p.S) * ngk;
         const int64_t wq = (nq + TPW - 1) / TPW, wk = (nk + TPW - 1) / TPW;
-        int64_t w = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+        // wave-uniform (scalar) wave index: kind, task and the gamma / table
+        // pointers are then chosen in scalar registers, not by per-lane selects
+        // that turn kernel-argument reads into vector loads (and a wait for
+        // every load in flight)
+        int64_t w = int64_t(blockIdx.x) * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         int kind;
         int64_t t0, n_kind;
         int ng;
@@ -175,12 +191,15 @@ struct Append {
         if (kind < 2) {
             const bool is_q = kind == 0;
             const int H = is_q ? p.Hq : p.Hkv;
-            // Every load of the wave is issued before any arithmetic: the rows,
-            // gamma (once) and the RoPE table chunks of each row's position.
+            // Every load of the wave is issued before any arithmetic: the K page
+            // ids first (the address is formed from the first load to land; the
+            // load counter is in order), then the rows, gamma (once) and the
+            // RoPE table chunks of each row's position.
             uint2 x[TPW][R];
             float4 c4[TPW][TR], s4[TPW][TR];
             int tok[TPW], h[TPW];
             bool ok[TPW];
+            int32_t id_args[TPW], id_table[TPW];  // K: the two candidates of the page id
             const bool rope = p.cos_tab != nullptr;
 #pragma unroll
             for (int u = 0; u < TPW; ++u) {
@@ -188,6 +207,18 @@ struct Append {
                 tok[u] = int(t / ng);
                 h[u] = int(t - int64_t(tok[u]) * ng) * 8 + r;
                 ok[u] = t < n_kind && h[u] < H;
+                id_args[u] = id_table[u] = -1;
+                // the token (not the row) picks the page: a wave-uniform load, no divergent branch
+                if (!is_q) page_id_loads(p, (p.pos0 + (t < n_kind ? tok[u] : 0)) / kPage, 0, id_args[u], id_table[u]);
+            }
+            const float* gamma = is_q ? p.gamma_q : p.gamma_k;
+            float4 gw[R];
+            if (gamma) {
+#pragma unroll
+                for (int c = 0; c < R; ++c) gw[c] = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < TPW; ++u) {
                 const uint16_t* src = is_q ? p.q + tok[u] * p.q_tok_stride + h[u] * p.q_head_stride
                                            : p.k + tok[u] * p.k_tok_stride + h[u] * p.k_head_stride;
 #pragma unroll
@@ -206,19 +237,20 @@ struct Append {
                     }
                 }
             }
-            const float* gamma = is_q ? p.gamma_q : p.gamma_k;
-            float4 gw[R];
-            if (gamma) {
+            // the page ids are used only now, with every load of the wave in flight
+            uint16_t* dsts[TPW];
 #pragma unroll
-                for (int c = 0; c < R; ++c) gw[c] = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * c);
+            for (int u = 0; u < TPW; ++u) {
+                __asm__ volatile("" : "+v"(id_args[u]), "+v"(id_table[u])::"memory");
+                dsts[u] = !ok[u] ? nullptr
+                          : is_q ? p.q_out + tok[u] * p.qo_tok_stride + h[u] * p.qo_head_stride
+                                 : k_dst(p, tok[u], h[u], id_args[u], id_table[u]);
             }
 #pragma unroll
             for (int u = 0; u < TPW; ++u) {
                 if (t0 + u >= n_kind) break;  // wave-uniform
                 norm_rope(x[u], gamma != nullptr, gw, p.eps, rope, c4[u], s4[u]);
-                if (!ok[u]) continue;
-                uint16_t* dst = is_q ? p.q_out + tok[u] * p.qo_tok_stride + h[u] * p.qo_head_stride
-                                     : k_dst(p, tok[u], h[u]);
+                uint16_t* const dst = dsts[u];
                 if (!dst) continue;
                 if (is_q) {  // q_out is read by the attention kernel right after: plain stores keep it cached
 #pragma unroll
