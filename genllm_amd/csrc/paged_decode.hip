@@ -10,9 +10,10 @@
 // The kv head is the fastest grid index: the dispatcher deals workgroups to the
 // 8 XCDs round-robin, so with 8 kv heads every split of head h (and, with the
 // same order in the merge grid, that head's merge) runs on XCD h.  8 waves
-// serve short page ranges (at most kWideMaxPps pages, D = 128): each wave then
-// owns at most 4 pages, so a split finishes in fewer dependent memory round
-// trips.  Long ranges keep 4 waves, which holds fewer bytes in flight per CU.  The rows of the kv head -- its (query, GQA q-head) pairs, at
+// serve ranges of up to kWideMaxPps pages at D = 128 (config 3's 32 and config
+// 5's 64-65): each wave then owns half the pages of a 4-wave form, so a split
+// finishes in fewer dependent memory round trips.  Longer ranges, and D = 256,
+// keep 4 waves.  The rows of the kv head -- its (query, GQA q-head) pairs, at
 // most 16 -- are the 16 columns of the MFMA tiles, so K/V are read once for all
 // of them.
 //
@@ -53,7 +54,10 @@ namespace {
 constexpr int kRows = 16;      // rows (query x q-head pairs) per kv head
 constexpr int kWaves = 4;       // waves of a split workgroup (long page ranges)
 constexpr int kWideWaves = 8;   // waves of a split workgroup over short ranges (D = 128)
-constexpr int kWideMaxPps = 32; // pages per split up to which the 8-wave form runs
+// pages per split up to which the 8-wave form runs (measured at config 5, 64
+// pages: 29.5 against 31.0 us per layer with 4 waves, and 30.1 against 31.2
+// for the captured decode step, whose plan covers 65)
+constexpr int kWideMaxPps = 128;
 constexpr int kMergeU = 16;     // splits in flight per merge lane
 constexpr int kMergeDims = 64;  // dims per merge workgroup
 constexpr int kMaxSplits = 256;
