@@ -112,9 +112,9 @@ def test_decode_split_plans(orc, pps):
     ctx.close()
 
 
-@pytest.mark.parametrize("pps", [17, 32, 33, 64])
+@pytest.mark.parametrize("pps", [17, 32, 64, 128, 129, 200])
 def test_decode_wave_forms(orc, pps):
-    """Head_dim 128 splits of at most 32 pages run 8-wave workgroups, longer
+    """Head_dim 128 splits of at most 128 pages run 8-wave workgroups, longer
     ones 4 waves; both forms against the oracle over 4100 keys (257 pages,
     the last one partial), with a fresh and a stale workspace."""
     ctx = Context(orc, 8, 128, 300, 4100, 91 + pps, nan_tail=True)
