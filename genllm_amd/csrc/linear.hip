@@ -173,14 +173,58 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_kernel(const uint16_
 // through the L1.  Here the workgroup's weight rows -- cpw whole columns, one
 // contiguous range -- come in with LDS-mode buffer loads of 1 KB per wave
 // instruction, x once per workgroup the same way, and each lane then reads its
-// block from LDS.  Block P of the workgroup (lane pair P: column P / nb, block
-// P % nb, as in linear_gemv_kernel) is stored rotated by 2P chunks of 16 B
-// (chunk q at position (q + 2P) % 32), x's block b by 2b, so that the 16 lanes
-// of a read phase hit 16 different bank groups.  The multiply-add order and the
+// block from LDS.  Lane pair P works on block P of the workgroup (column
+// P / nb, block P % nb, as in linear_gemv_kernel).
+//
+// The weights arrive in four parts: part k holds bytes 128k..128k+127 of every
+// block (its 16-byte chunks 8k..8k+7, the lane pair's iterations 4k..4k+3), and
+// the parts are requested in order after x.  Each wave waits only for the
+// parts it is about to use, and the workgroup multiplies part k while the later
+// parts are still arriving; only the last part's multiply-adds follow the last
+// load (Qwen3-4B projection: 8.3 against 9.0 us with one wait for everything,
+// 8.5 with two halves; A/B on one box, results bit-identical).
+//
+// LDS: part k is a region of 128-byte slots, slot P holding part k of block P
+// with chunk q at position (q + 2 (P / 2)) % 8; x rows follow, block b rotated
+// by 2b chunks of 16 B (chunk q at (q + 2b) % 32).  A read phase of 16 lanes
+// (8 lane pairs: even and odd slots fill the two 128-byte halves of the 64
+// banks) then hits 16 different bank groups.  The multiply-add order and the
 // block sums are those of linear_gemv_kernel.  Loads past the weights or x (the
-// last workgroup, an odd block count) are bounded by the buffer resources and
-// read zeros into LDS slots no lane reads.  (Measured against block-major slots,
-// whose read phases share x's block, and x staged as fp32: both slower.)
+// last workgroup, a block count that does not fill a load) are bounded by the
+// buffer resources and read zeros into LDS slots no lane reads.  (Measured
+// against block-major slots, whose read phases share x's block, and x staged
+// as fp32: both slower.)
+constexpr int kGemvParts = 4;
+constexpr int kGemvPartBlocks = 8;  // 128-byte part slots per 1 KB load
+__host__ __device__ constexpr size_t gemv_lds_bytes(int rows, int n_pairs, int nb) {
+    return size_t(kGemvParts) * ((n_pairs + kGemvPartBlocks - 1) / kGemvPartBlocks) * 1024 +
+           size_t(rows) * ((nb + 1) / 2) * 1024;
+}
+
+// s_waitcnt vmcnt(n) for the n a wave computes at run time (the count is an
+// instruction immediate); counts past 15 wait for everything
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 0); break;
+        case 1: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 1); break;
+        case 2: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 2); break;
+        case 3: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 3); break;
+        case 4: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 4); break;
+        case 5: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 5); break;
+        case 6: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 6); break;
+        case 7: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 7); break;
+        case 8: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 8); break;
+        case 9: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 9); break;
+        case 10: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 10); break;
+        case 11: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 11); break;
+        case 12: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 12); break;
+        case 13: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 13); break;
+        case 14: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 14); break;
+        case 15: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | 15); break;
+        default: __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); break;
+    }
+}
+
 template <int R>
 __global__ __launch_bounds__(kGemvThreads) void linear_gemv_lds_kernel(const uint16_t* __restrict__ x,
                                                                        const uint16_t* __restrict__ w,
@@ -193,10 +237,12 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_lds_kernel(const uin
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     constexpr int kWaves = kGemvThreads / 64;
     const int col0 = int(blockIdx.x) * cpw;
-    const int n_pairs = cpw * nb;                 // 512-byte blocks of this workgroup
-    const int w_inst = (n_pairs + 1) / 2;         // 1 KB loads of them
-    const int x_inst = (nb + 1) / 2;              // 1 KB loads per row of x
-    const int x_base = w_inst * 1024;             // x rows after the weights
+    const int n_pairs = cpw * nb;                                          // 512-byte blocks of this workgroup
+    const int part_inst = (n_pairs + kGemvPartBlocks - 1) / kGemvPartBlocks;  // 1 KB loads per part
+    const int part_bytes = part_inst * 1024;
+    const int x_inst = (nb + 1) / 2;                                       // 1 KB loads per row of x
+    const int x_base = kGemvParts * part_bytes;                            // x rows after the weights
+    int n_part = 0;                                                        // this wave's loads per part
     {
         const int64_t left = int64_t(cols - col0) * common * 2;
         const uint32_t span = uint32_t(min<int64_t>(left, int64_t(n_pairs) * 512));
@@ -205,43 +251,57 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_lds_kernel(const uin
         const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, uint32_t(R * common * 2),
                                                           kBufferFlags);
         const int half = lane >> 5, pos = lane & 31;  // block of the 1 KB, LDS chunk position in it
-        for (int e = wv; e < w_inst; e += kWaves) {
-            const int P = 2 * e + half;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(lds_w + e * 1024),
-                                                     16, uint32_t(P * 512 + ((pos - 2 * P) & 31) * 16), 0, 0, 0);
-        }
         for (int e = wv; e < R * x_inst; e += kWaves) {
             const int r = e / x_inst, bb = 2 * (e - r * x_inst) + half;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rx, (__attribute__((address_space(3))) void*)(lds_w + x_base + e * 1024), 16,
                 uint32_t(r * common * 2 + bb * 512 + ((pos - 2 * bb) & 31) * 16), 0, 0, 0);
         }
+        const int slot = lane >> 3, p8 = lane & 7;  // part slot of the 1 KB, LDS chunk position in it
+#pragma unroll
+        for (int k = 0; k < kGemvParts; ++k)
+            for (int e = wv; e < part_inst; e += kWaves) {
+                const int P = kGemvPartBlocks * e + slot;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rw, (__attribute__((address_space(3))) void*)(lds_w + k * part_bytes + e * 1024), 16,
+                    uint32_t(P * 512 + 128 * k + ((p8 - 2 * (P >> 1)) & 7) * 16), 0, 0, 0);
+                if (k == 0) ++n_part;
+            }
     }
     const int pair = t >> 1, h = t & 1;
     const int lc = pair / nb, b = pair - lc * nb;  // column within the workgroup, block
     const bool item = pair < n_pairs && col0 + lc < cols;
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
 
     float s[R][8];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int l = 0; l < 8; ++l) s[r][l] = 0.0f;
-    if (item) {
-        const char* wl = lds_w + pair * 512;
-        const char* xl = lds_w + x_base + b * 512;
+    const char* xl = lds_w + x_base + b * 512;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int q = 2 * i + h;
-            float wf[8];
-            bf16x8_to_f32(*reinterpret_cast<const uint4*>(wl + ((q + 2 * pair) & 31) * 16), wf);
+    for (int k = 0; k < kGemvParts; ++k) {
+        // this wave's loads of parts past k may still be in flight; the other
+        // waves' loads of parts up to k have landed once they reach the
+        // barrier.  A bare barrier: a fence would wait for every load.
+        wait_vmcnt(n_part * (kGemvParts - 1 - k));
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (item) {
+            const char* wl = lds_w + k * part_bytes + pair * 128;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float xf[8];
-                bf16x8_to_f32(*reinterpret_cast<const uint4*>(xl + r * x_inst * 1024 + ((q + 2 * b) & 31) * 16), xf);
+            for (int i = 0; i < 4; ++i) {
+                const int q = 2 * i + h;  // chunk within the part (chunk 8k + q of the block)
+                float wf[8];
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(wl + ((q + 2 * (pair >> 1)) & 7) * 16), wf);
 #pragma unroll
-                for (int l = 0; l < 8; ++l) s[r][l] = __builtin_fmaf(xf[l], wf[l], s[r][l]);
+                for (int r = 0; r < R; ++r) {
+                    float xf[8];
+                    bf16x8_to_f32(
+                        *reinterpret_cast<const uint4*>(xl + r * x_inst * 1024 + ((8 * k + q + 2 * b) & 31) * 16), xf);
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) s[r][l] = __builtin_fmaf(xf[l], wf[l], s[r][l]);
+                }
             }
         }
     }
@@ -325,7 +385,7 @@ int launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, ui
         const int cpw = kGemvThreads / (2 * nb);
         const unsigned grid = unsigned((cols + cpw - 1) / cpw);
         const int c = int(common), n = int(cols);
-        const size_t lds = size_t((cpw * nb + 1) / 2) * 1024 + size_t(rows) * ((nb + 1) / 2) * 1024;
+        const size_t lds = gemv_lds_bytes(int(rows), cpw * nb, nb);
         if (common % kBlockK == 0 && lds <= kGemvLdsMax) {
             switch (rows) {
                 case 1: hipLaunchKernelGGL(linear_gemv_lds_kernel<1>, dim3(grid), dim3(kGemvThreads), lds, stream, x, w, bias, out, c, n, nb, cpw); break;

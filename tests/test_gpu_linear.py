@@ -52,7 +52,10 @@ def inputs(seed, rows, common, cols, wscale=0.05):
     (3, 512, 77),      # the last workgroup holds 13 of its 64 columns
     (2, 1280, 101),    # 5 blocks per column: an odd block count per workgroup (125)
     (1, 4096, 130),
-    (2, 8192, 64),     # 80 KB of LDS: the largest staged shape
+    (1, 8192, 64),     # 80 KB of LDS: the largest staged shape
+    (2, 8192, 64),     # 96 KB of LDS: the direct-load kernel
+    (1, 768, 97),      # 3 blocks per column: 126 blocks per workgroup, the last 1 KB load of each part half full
+    (3, 1792, 50),     # 7 blocks per column: 126 blocks, 3 rows of x
 ])
 def test_linear_gemv_bit_exact(orc, rows, common, cols):
     x, w, b = inputs(rows * 1000 + common + cols, rows, common, cols)
