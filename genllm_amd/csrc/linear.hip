@@ -181,8 +181,9 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_kernel(const uint16_
 // the parts are requested in order after x.  Each wave waits only for the
 // parts it is about to use, and the workgroup multiplies part k while the later
 // parts are still arriving; only the last part's multiply-adds follow the last
-// load (Qwen3-4B projection: 8.3 against 9.0 us with one wait for everything,
-// 8.5 with two halves; A/B on one box, results bit-identical).
+// load (Qwen3-4B projection: 8.2-8.3 against 9.0 us with one wait for
+// everything, 8.5 with two halves, 9.3 with eight parts; A/B on one box,
+// results bit-identical).
 //
 // LDS: part k is a region of 128-byte slots, slot P holding part k of block P
 // with chunk q at position (q + 2 (P / 2)) % 8; x rows follow, block b rotated
@@ -195,7 +196,9 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_kernel(const uint16_
 // against block-major slots, whose read phases share x's block, and x staged
 // as fp32: both slower.)
 constexpr int kGemvParts = 4;
-constexpr int kGemvPartBlocks = 8;  // 128-byte part slots per 1 KB load
+constexpr int kGemvPartChunks = 32 / kGemvParts;          // 16-byte chunks of a block per part
+constexpr int kGemvPartBlocks = 64 / kGemvPartChunks;     // part slots per 1 KB load
+constexpr int kGemvRotShift = kGemvParts == 2 ? 0 : kGemvParts == 4 ? 1 : 2;  // slot pairs, quads per rotation step
 __host__ __device__ constexpr size_t gemv_lds_bytes(int rows, int n_pairs, int nb) {
     return size_t(kGemvParts) * ((n_pairs + kGemvPartBlocks - 1) / kGemvPartBlocks) * 1024 +
            size_t(rows) * ((nb + 1) / 2) * 1024;
@@ -257,14 +260,15 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_lds_kernel(const uin
                 rx, (__attribute__((address_space(3))) void*)(lds_w + x_base + e * 1024), 16,
                 uint32_t(r * common * 2 + bb * 512 + ((pos - 2 * bb) & 31) * 16), 0, 0, 0);
         }
-        const int slot = lane >> 3, p8 = lane & 7;  // part slot of the 1 KB, LDS chunk position in it
+        constexpr int CH = kGemvPartChunks;
+        const int slot = lane / CH, pc = lane % CH;  // part slot of the 1 KB, LDS chunk position in it
 #pragma unroll
         for (int k = 0; k < kGemvParts; ++k)
             for (int e = wv; e < part_inst; e += kWaves) {
                 const int P = kGemvPartBlocks * e + slot;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     rw, (__attribute__((address_space(3))) void*)(lds_w + k * part_bytes + e * 1024), 16,
-                    uint32_t(P * 512 + 128 * k + ((p8 - 2 * (P >> 1)) & 7) * 16), 0, 0, 0);
+                    uint32_t(P * 512 + (CH * k + ((pc - 2 * (P >> kGemvRotShift)) & (CH - 1))) * 16), 0, 0, 0);
                 if (k == 0) ++n_part;
             }
     }
@@ -278,33 +282,47 @@ __global__ __launch_bounds__(kGemvThreads) void linear_gemv_lds_kernel(const uin
 #pragma unroll
         for (int l = 0; l < 8; ++l) s[r][l] = 0.0f;
     const char* xl = lds_w + x_base + b * 512;
+    // part k's multiply-adds: chunks CH k .. CH k + CH - 1 of the lane's block
+    auto run_part = [&](int k) {
+        constexpr int CH = kGemvPartChunks;
+        const char* wl = lds_w + k * part_bytes + pair * (CH * 16);
 #pragma unroll
-    for (int k = 0; k < kGemvParts; ++k) {
-        // this wave's loads of parts past k may still be in flight; the other
-        // waves' loads of parts up to k have landed once they reach the
-        // barrier.  A bare barrier: a fence would wait for every load.
+        for (int i = 0; i < CH / 2; ++i) {
+            const int q = 2 * i + h;  // chunk within the part
+            float wf[8];
+            bf16x8_to_f32(*reinterpret_cast<const uint4*>(wl + ((q + 2 * (pair >> kGemvRotShift)) & (CH - 1)) * 16),
+                          wf);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float xf[8];
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(xl + r * x_inst * 1024 + ((CH * k + q + 2 * b) & 31) * 16),
+                              xf);
+#pragma unroll
+                for (int l = 0; l < 8; ++l) s[r][l] = __builtin_fmaf(xf[l], wf[l], s[r][l]);
+            }
+        }
+    };
+    // wait until part k has landed: this wave's loads of the later parts may
+    // still be in flight, and the other waves' loads of parts up to k have
+    // landed once they reach the barrier.  A bare barrier: a fence would wait
+    // for every load.
+    auto part_ready = [&](int k) {
         wait_vmcnt(n_part * (kGemvParts - 1 - k));
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        if (item) {
-            const char* wl = lds_w + k * part_bytes + pair * 128;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int q = 2 * i + h;  // chunk within the part (chunk 8k + q of the block)
-                float wf[8];
-                bf16x8_to_f32(*reinterpret_cast<const uint4*>(wl + ((q + 2 * (pair >> 1)) & 7) * 16), wf);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float xf[8];
-                    bf16x8_to_f32(
-                        *reinterpret_cast<const uint4*>(xl + r * x_inst * 1024 + ((8 * k + q + 2 * b) & 31) * 16), xf);
-#pragma unroll
-                    for (int l = 0; l < 8; ++l) s[r][l] = __builtin_fmaf(xf[l], wf[l], s[r][l]);
-                }
-            }
-        }
-    }
+    };
+    // (written out: the same sequence as a loop over k measured 8.65 against
+    // 8.3 us -- the compiler then kept one LDS read in flight at a time)
+    static_assert(kGemvParts == 4, "the part sequence below is written for four parts");
+    part_ready(0);
+    if (item) run_part(0);
+    part_ready(1);
+    if (item) run_part(1);
+    part_ready(2);
+    if (item) run_part(2);
+    part_ready(3);
+    if (item) run_part(3);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float v[8];
