@@ -20,12 +20,12 @@
 // swizzled per 256-byte half: chunk c of row r sits at position
 // 16 (c / 16) + ((c % 16) ^ swz(r % 16)), with swz(r) = 2 ((r % 8) ^ 4 (r / 8))
 // + r / 8.
-// Wave w < 4 moves the K (w even) or V (w odd) rows of pages w / 2 and w / 2 + 2
-// of every tile straight from HBM into LDS with 16-byte buffer loads in LDS
-// mode (lane i's 16 bytes land at base + 16 i), so a tile costs no registers,
-// no VALU and no LDS store instructions; one buffer resource per page (base = the page of
-// this kv head, size = the bytes its rows below the key limit span) bounds
-// every load.
+// Wave w < 4 moves the K (w even) or V (w odd) rows of pages w / 2 and
+// w / 2 + 2 of every tile straight from HBM into LDS with 16-byte buffer loads
+// in LDS mode (lane i's 16 bytes land at base + 16 i), so a tile costs no
+// registers, no VALU and no LDS store instructions; one buffer resource per
+// page (base = the page of this kv head, size = the bytes its rows below the
+// key limit span) bounds every load.  Waves 4-7 issue no loads.
 // Per tile and wave:
 //   S^T = K Q^T  (v_mfma_f32_16x16x32_bf16 x 2 D/32; A = K from LDS: lane l ->
 //        key l%16, dims 32ks+8(l/16)..; B = Q^T held in registers).
@@ -166,7 +166,7 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
     // ---- staging: wave w < 4 moves kind w % 2 (K, V) of pages w / 2 and
     // w / 2 + 2 of each tile; waves 4-7 issue no tile loads.  Waves 4-7 share
     // their SIMDs with waves 0-3 and reach their S^T MFMAs after them, so the
-    // step waits for them: keeping the 8 loads' issue off their path measured
+    // step waits for them: keeping the loads' issue off their path measured
     // 31.3 against 31.5 us at config 4 and 48.9 against 50.2 us at head_dim 256
     // (A/B on one box; the mirror split, waves 4-7 loading, 32.2 and 50.7).
     const bool paged = p.k_ids != nullptr;
