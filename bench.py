@@ -27,9 +27,10 @@ replayed as one HIP graph), and the Qwen3-4B fused Q/K/V projection feeding
 the path (decode GEMV GB/s, 2048-token GEMM TFLOPS).  cpu_baseline = the
 oracle (single thread) on a bounded sample of the headline workload.
 
---only {headline,append,prefill,flash,qwen35,longctx,linear,copy,traffic} runs
-one workload alone (for rocprofv3 passes); the line then carries only that
-workload's figures.  --no-traffic skips the child counter passes (they are
+--only {headline,append,prefill,flash,qwen35,longctx,linear,copy,traffic,
+prefill_scale} runs one workload alone (for rocprofv3 passes); the line then
+carries only that workload's figures.  prefill_scale (the prefill kernel at
+2K-16K tokens) runs only this way.  --no-traffic skips the child counter passes (they are
 skipped anyway when the bench itself runs under rocprofv3).
 """
 from __future__ import annotations
@@ -64,7 +65,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
     ap.add_argument("--only", choices=["headline", "append", "prefill", "flash", "qwen35", "longctx", "linear", "copy",
-                                       "traffic"], default=None)
+                                       "traffic", "prefill_scale"], default=None)
     ap.add_argument("--no-traffic", action="store_true", help="skip the child rocprofv3 --pmc traffic passes")
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -317,6 +318,30 @@ def flash_cfg4(np, torch, paged, synth, call, iters=40):
     tfl = flops / (avg_us * 1e-6) / 1e12
     return {"avg_launch_us": round(avg_us, 3), "flops": flops, "TFLOPS": round(tfl, 1),
             "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)}
+
+
+def prefill_scale(np, torch, paged, synth, call, iters=10):
+    """The prefill kernel (FlashAttention form, causal) past config 4's size:
+    the same kernel at 2K-16K tokens for Qwen3 head counts and at head_dim 256.
+    Not part of the default run (bench.py --only prefill_scale)."""
+    out = []
+    for i, (Hq, Hkv, S, D) in enumerate([(16, 8, 2048, 128), (32, 8, 2048, 128), (16, 8, 4096, 128),
+                                         (32, 8, 8192, 128), (16, 8, 16384, 128), (8, 2, 2048, 256),
+                                         (8, 2, 8192, 256)]):
+        q = torch.empty((1, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+        k = torch.empty((1, Hkv, S, D), dtype=torch.bfloat16, device="cuda")
+        v = torch.empty_like(k)
+        paged.fill_normal_bf16(q, 7000 + 3 * i)
+        paged.fill_normal_bf16(k, 7001 + 3 * i)
+        paged.fill_normal_bf16(v, 7002 + 3 * i)
+        o = torch.empty_like(q)
+        avg_us = time_kernels(torch, lambda _: paged.flash_attention(q, k, v, o, Hq // Hkv, 1.0 / np.sqrt(D)), iters)
+        flops = 4 * D * Hq * S * (S + 1) // 2
+        tfl = flops / (avg_us * 1e-6) / 1e12
+        out.append({"q_heads": Hq, "kv_heads": Hkv, "S": S, "head_dim": D, "avg_launch_us": round(avg_us, 2),
+                    "TFLOPS": round(tfl, 1), "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)})
+        del q, k, v, o
+    return {"shapes": out}
 
 
 def qwen35_d256(np, torch, paged, synth, call, iters=100):
@@ -667,7 +692,8 @@ def main():
         return
     if args.only and args.only != "headline":
         fn = {"append": append_cfg2, "prefill": prefill_cfg4, "flash": flash_cfg4, "qwen35": qwen35_d256,
-              "longctx": longctx_cfg5, "linear": linear_qkv, "copy": copy_calibration}[args.only]
+              "longctx": longctx_cfg5, "linear": linear_qkv, "copy": copy_calibration,
+              "prefill_scale": prefill_scale}[args.only]
         print(json.dumps({"only": args.only, **fn(*common)}), flush=True)
         return
 
