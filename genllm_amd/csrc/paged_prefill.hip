@@ -7,9 +7,12 @@
 //
 // Grid: query tiles of 64 rows x Hq workgroups of 8 waves: the long half of
 // the query tiles from the last down, then the short half from the first up.
-// Wave (qb, kh) owns query block qb (16 queries) of the tile and key half kh
-// (32 keys) of every key tile of 64 tokens (4 pages);
-// the two halves of a query block are merged through LDS at the end.  At
+// Wave w = qb + 4 kh owns query block qb (16 queries) of the tile and key
+// half kh (32 keys) of every key tile of 64 tokens (4 pages), so the two key
+// halves of a query block share a SIMD (waves w and w + 4; measured 30.9
+// against 31.5 us at config 4 and 47.4 against 48.1 us at head_dim 256 with
+// the halves of two query blocks paired instead); the two halves of a query
+// block are merged through LDS at the end.  At
 // head_dim 128 a workgroup holds 64 KB of LDS and at most 128 VGPRs per lane,
 // so two workgroups share a CU (4 waves per SIMD: one workgroup's barrier
 // waits and dependent chains are filled by the other's work); the grid's
@@ -119,7 +122,7 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int qblk = wv >> 1, kh = wv & 1;  // query block, key half
+    const int qblk = wv & 3, kh = wv >> 2;  // query block, key half (waves w and w + 4 share a SIMD)
     const int n16 = lane & 15, g = lane >> 4;
     const int n_qt = (p.S + QT - 1) / QT;
     const int rank = int(blockIdx.x) / p.Hq;
