@@ -23,10 +23,10 @@
 // swizzled per 256-byte half: chunk c of row r sits at position
 // 16 (c / 16) + ((c % 16) ^ swz(r % 16)), with swz(r) = 2 ((r % 8) ^ 4 (r / 8))
 // + r / 8.
-// Wave w < 4 moves the K (w even) or V (w odd) rows of pages w / 2 and
-// w / 2 + 2 of every tile straight from HBM into LDS with 16-byte buffer loads
-// in LDS mode (lane i's 16 bytes land at base + 16 i), so a tile costs no
-// registers, no VALU and no LDS store instructions; one buffer resource per
+// Wave w < 4 moves the K rows, then the V rows of page w of every tile
+// straight from HBM into LDS with 16-byte buffer loads in LDS mode (lane i's
+// 16 bytes land at base + 16 i), so a tile costs no registers, no VALU and no
+// LDS store instructions; one buffer resource per
 // page (base = the page of this kv head, size = the bytes its rows below the
 // key limit span) bounds every load.  Waves 4-7 issue no loads.
 // Per tile and wave:
@@ -166,24 +166,25 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
     const int wave_lim = p.causal ? min(qabs0 + q0 + 1, n_cached) : n_cached;
     const int wave_end = !wave_has_rows ? 0 : p.causal ? min(qabs0 + min(q0 + QW, p.S), n_cached) : n_cached;
 
-    // ---- staging: wave w < 4 moves kind w % 2 (K, V) of pages w / 2 and
-    // w / 2 + 2 of each tile; waves 4-7 issue no tile loads.  Waves 4-7 share
-    // their SIMDs with waves 0-3 and reach their S^T MFMAs after them, so the
-    // step waits for them: keeping the loads' issue off their path measured
-    // 31.3 against 31.5 us at config 4 and 48.9 against 50.2 us at head_dim 256
-    // (A/B on one box; the mirror split, waves 4-7 loading, 32.2 and 50.7).
+    // ---- staging: wave w < 4 moves page w of each tile, its K rows, then its
+    // V rows; waves 4-7 issue no tile loads.  Waves 4-7 share their SIMDs
+    // with waves 0-3 and reach their S^T MFMAs after them, so the step waits
+    // for them: keeping the loads' issue off their path measured 31.3 against
+    // 31.5 us at config 4 and 48.9 against 50.2 us at head_dim 256 (A/B on one
+    // box; the mirror split, waves 4-7 loading, 32.2 and 50.7).  Every K row
+    // of the tile is requested before any V row (needed first): 30.6 against
+    // 30.9 us at config 4, 47.0 against 47.3 at head_dim 256, against one
+    // kind per wave over two pages.
     const bool paged = p.k_ids != nullptr;
-    const int kind = wv & 1, pg = (wv >> 1) & 1;
+    const int pg = wv & 3;  // this wave's page of the tile (waves 0-3)
     const bool dma_wave = wv < 4;
-    const int32_t* const my_ids = kind ? p.v_ids : p.k_ids;
     const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
-    const uint16_t* const src = (kind ? p.v_pool : p.k_pool) + head_off;
     const int64_t kv_row = p.kv_row, page_elems = p.page_elems;
     const int kv_row_bytes = int(kv_row) * 2;
-    // lane i <- the id of page pgx of tile t0 + i
-    auto load_ids = [&](int t0, int pgx) -> int {
-        const int page = 4 * (t0 + lane) + pgx;
-        return page * kPage < kv_end ? my_ids[page] : 0;
+    // lane i <- the K (kindx 0) or V (1) id of page pg of tile t0 + i
+    auto load_ids = [&](int t0, int kindx) -> int {
+        const int page = 4 * (t0 + lane) + pg;
+        return page * kPage < kv_end ? (kindx ? p.v_ids : p.k_ids)[page] : 0;
     };
     // instruction e fills rows RPI e .. RPI e + RPI-1 of the page (4 rows of
     // 256 B at D = 128, 2 of 512 B at D = 256): lane -> row RPI e + lane/LPR,
@@ -196,12 +197,13 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
         const int chunk = 16 * (pos >> 4) + ((pos & 15) ^ swz(row));
         dma_off[e] = uint32_t(row * kv_row_bytes + 16 * chunk);
     }
-    const int dst0 = kind * TILEB;
+
     // The buffer resource of a page spans exactly its rows below kv_end, so
     // rows past the causal limit, the cache end or the table read as zeros:
     // their keys are masked and their zero values meet zero probabilities.
-    auto issue_page = [&](int t, int ids, lds_char* buf, int pgx) {  // page pgx of tile t
-        const int tok_page = t * KT + kPage * pgx;
+    auto issue_page = [&](int t, int ids, lds_char* buf, int kindx) {  // K (0) or V (1) rows of page pg of tile t
+        const uint16_t* const src = (kindx ? p.v_pool : p.k_pool) + head_off;
+        const int tok_page = t * KT + kPage * pg;
         const int valid = min(max(kv_end - tok_page, 0), kPage);
         const uint32_t span = uint32_t(__builtin_amdgcn_readfirstlane(valid > 0 ? (valid - 1) * kv_row_bytes + ROWB : 0));
         const int64_t base = paged ? int64_t(__builtin_amdgcn_readlane(ids, t & (IDS_BLOCK - 1))) * page_elems
@@ -210,13 +212,13 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
 #pragma unroll
         for (int e = 0; e < NI; ++e)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                r, (__attribute__((address_space(3))) void*)(buf + (dst0 + pgx * (kPage * ROWB) + e * 1024)), 16,
+                r, (__attribute__((address_space(3))) void*)(buf + (kindx * TILEB + pg * (kPage * ROWB) + e * 1024)), 16,
                 dma_off[e], 0, 0, 0);
     };
-    auto issue_tile = [&](int t, int ids0, int ids1, lds_char* buf) {  // ids0, ids1: pages pg, pg + 2
+    auto issue_tile = [&](int t, int ids0, int ids1, lds_char* buf) {  // ids0, ids1: K and V ids of page pg
         if (dma_wave) {
-            issue_page(t, ids0, buf, pg);
-            issue_page(t, ids1, buf, pg + 2);
+            issue_page(t, ids0, buf, 0);
+            issue_page(t, ids1, buf, 1);
         }
     };
 
@@ -302,8 +304,8 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
     // in each of waves 0-3; a tile past the last one has no rows below kv_end and reads
     // as zeros.  Page ids arrive IDS_BLOCK tiles per load; the rare reload
     // drains the loads in flight.
-    int ids0 = paged && dma_wave ? load_ids(0, pg) : 0;
-    int ids1 = paged && dma_wave ? load_ids(0, pg + 2) : 0;
+    int ids0 = paged && dma_wave ? load_ids(0, 0) : 0;
+    int ids1 = paged && dma_wave ? load_ids(0, 1) : 0;
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // q and ids landed
     issue_tile(0, ids0, ids1, buf0);
     auto step = [&](int t, const lds_char* cur, lds_char* nxt) {
@@ -311,8 +313,8 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
         tile_barrier();
         if (((t + 1) & (IDS_BLOCK - 1)) == 0 && t + 1 < n_tiles) {
             if (paged && dma_wave) {
-                ids0 = load_ids(t + 1, pg);
-                ids1 = load_ids(t + 1, pg + 2);
+                ids0 = load_ids(t + 1, 0);
+                ids1 = load_ids(t + 1, 1);
             }
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         }
