@@ -227,7 +227,7 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
     // or past the cache end.
     const float c = fmaxf(p.scale_log2, __FLT_MIN__);  // > 0: masked -inf scores give exactly 0
     const float inv_c = 1.0f / c;                       // may be inf (then no row grows after its first tile)
-    auto compute_tile = [&](int t, const lds_char* buf, bool masked) {
+    auto compute_tile = [&](int t, const lds_char* buf, bool masked, auto&& after_s) {
         const int tok0 = t * KT + KH * kh;  // first key of the half
         const int r0 = KH * kh;             // its first LDS row (a multiple of 16)
         f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -241,6 +241,7 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
                     buf + (row * ROWB + pos * 16));
                 s[kb] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[ks], s[kb]);
             }
+        after_s();
         if (masked) {
             __asm__ volatile("");  // keep a branch: full tiles carry no selects
             const int qpos = qabs0 + q0 + n16;
@@ -318,9 +319,26 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
             }
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         }
-        issue_tile(t + 1, ids0, ids1, nxt);
+        // At head_dim 256 the next tile's V rows are requested after this
+        // tile's S^T MFMAs: the K reads right after the barrier then share the
+        // LDS with half the incoming rows, and the longer step still hides the
+        // V rows' latency (46.6-46.9 against 48.1-48.2 us at 2048 tokens; at
+        // head_dim 128 the step is too short: 32.6 against 30.4 us; A/B on
+        // one box).
+        constexpr bool late_v = D == 256;
+        if (late_v) {
+            if (dma_wave) issue_page(t + 1, ids0, nxt, 0);
+        } else {
+            issue_tile(t + 1, ids0, ids1, nxt);
+        }
+        auto issue_v = [&]() {
+            if (late_v && dma_wave) issue_page(t + 1, ids1, nxt, 1);
+        };
         const int tok0 = t * KT + KH * kh;
-        if (tok0 < wave_end) compute_tile(t, cur, tok0 + KH > wave_lim);
+        if (tok0 < wave_end)
+            compute_tile(t, cur, tok0 + KH > wave_lim, issue_v);
+        else
+            issue_v();
     };
     for (int t = 0; t < n_tiles; t += 2) {
         step(t, buf0, buf1);
