@@ -74,6 +74,39 @@ def test_flash_prefill_size_vs_torch():
         assert_attn_close(paged.to_host_bits(out[0, h]), want, f"flash 2048 head {h}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,S,D", [(32, 8, 8192, 128), (8, 2, 8192, 256)])
+def test_flash_long_vs_torch(Hq, Hkv, S, D):
+    """The prefill kernel at 8192 tokens (the bench's prefill_scale shapes),
+    causal: the first and last q heads against a float32 torch reference
+    computed on the GPU (float32 products: no bf16 batched matmul)."""
+    import torch
+
+    from genllm_amd import paged
+
+    print(f"flash long Hq{Hq} Hkv{Hkv} S{S} D{D}", flush=True)
+    scale = 1.0 / np.sqrt(D)
+    q = torch.empty((1, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    k = torch.empty((1, Hkv, S, D), dtype=torch.bfloat16, device="cuda")
+    v = torch.empty_like(k)
+    for i, t in enumerate((q, k, v)):
+        paged.fill_normal_bf16(t, 8800 + 10 * D + i)
+    out = torch.empty_like(q)
+    paged.flash_attention(q, k, v, out, Hq // Hkv, scale, True)
+    torch.cuda.synchronize()
+    mask = torch.triu(torch.ones(S, S, dtype=torch.bool, device="cuda"), 1)
+    G = Hq // Hkv
+    for h in (0, Hq - 1):
+        qf = q[0, h].float()
+        kf = k[0, h // G].float()
+        vf = v[0, h // G].float()
+        s = (qf @ kf.T.contiguous()) * scale
+        s.masked_fill_(mask, float("-inf"))
+        ref = torch.softmax(s, dim=-1) @ vf
+        want = ref.to(torch.bfloat16).cpu().view(torch.int16).numpy().view(np.uint16)
+        assert_attn_close(paged.to_host_bits(out[0, h]), want, f"flash {S} D{D} head {h}")
+        del s, ref
+
+
 @pytest.mark.parametrize("S,causal", [(77, True), (200, False), (1, True)])
 def test_flash_head_dim_256_vs_oracle(orc, S, causal):
     """Qwen3.5 attention shape (head_dim 256, 8 q / 2 kv heads) without paging."""
