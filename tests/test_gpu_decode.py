@@ -103,6 +103,18 @@ def test_decode_shapes(orc, Hq, Hkv, N):
     ctx.close()
 
 
+def test_decode_very_long_context(orc):
+    """131,073 cached keys (8,193 pages of a shuffled 8,200-page pool, the
+    last page holding one key): the default plan gives 257 pages per split,
+    the 4-wave form with 32+ page ids per wave."""
+    N, pool = 131073, 8200
+    ctx = Context(orc, 8, 128, pool, N, 131000, nan_tail=True)
+    q = synth.normal_bf16(131001, (32, 1, 128))
+    got, _ = ctx.decode(q)
+    assert_attn_close(got, ctx.oracle(q), f"N{N}")
+    ctx.close()
+
+
 @pytest.mark.parametrize("pps", [1, 2, 4, 8, 1000])
 def test_decode_split_plans(orc, pps):
     ctx = Context(orc, 8, 128, 80, 1000, 77)
