@@ -28,9 +28,10 @@ the path (decode GEMV GB/s, 2048-token GEMM TFLOPS).  cpu_baseline = the
 oracle (single thread) on a bounded sample of the headline workload.
 
 --only {headline,append,prefill,flash,qwen35,longctx,linear,copy,traffic,
-prefill_scale} runs one workload alone (for rocprofv3 passes); the line then
-carries only that workload's figures.  prefill_scale (the prefill kernel at
-2K-16K tokens) runs only this way.  --no-traffic skips the child counter passes (they are
+prefill_scale,decode_scale} runs one workload alone (for rocprofv3 passes);
+the line then carries only that workload's figures.  prefill_scale (the
+prefill kernel at 2K-16K tokens) and decode_scale (the decode kernels at
+8K-256K keys) run only this way.  --no-traffic skips the child counter passes (they are
 skipped anyway when the bench itself runs under rocprofv3).
 """
 from __future__ import annotations
@@ -65,7 +66,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
     ap.add_argument("--only", choices=["headline", "append", "prefill", "flash", "qwen35", "longctx", "linear", "copy",
-                                       "traffic", "prefill_scale"], default=None)
+                                       "traffic", "prefill_scale", "decode_scale"], default=None)
     ap.add_argument("--no-traffic", action="store_true", help="skip the child rocprofv3 --pmc traffic passes")
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -341,6 +342,48 @@ def prefill_scale(np, torch, paged, synth, call, iters=10):
         out.append({"q_heads": Hq, "kv_heads": Hkv, "S": S, "head_dim": D, "avg_launch_us": round(avg_us, 2),
                     "TFLOPS": round(tfl, 1), "frac_bf16_peak": round(tfl / BF16_PEAK_TFLOPS, 4)})
         del q, k, v, o
+    return {"shapes": out}
+
+
+def decode_scale(np, torch, paged, synth, call, iters=40):
+    """The decode kernel pair (stateless genllm_paged_decode, Qwen3-4B heads)
+    from 8K to 256K cached keys, each layer in its own shuffled pool; enough
+    layers rotate that the MALL cannot hold them.  Not part of the default
+    run (bench.py --only decode_scale)."""
+    Hq, Hkv, D = HQ3, HKV3, D3
+    out = []
+    for n_keys in (8193, 32761, 131073, 262145):
+        n_pages = (n_keys + PAGE - 1) // PAGE
+        pool = n_pages + 8
+        layer_bytes = 2 * pool * PAGE * Hkv * D * 2
+        L = max(1, -(-(1 << 30) // layer_bytes))
+        mgr = paged.PagedAttentionManager(L * layer_bytes + (1 << 20))
+        for l in range(L):
+            mgr.init_layer(l, Hkv, D)
+            mgr.reserve_layer(l, pool)
+            mgr.fragment(l, synth.shuffled(5000 + 2 * l, pool), synth.shuffled(5001 + 2 * l, pool))
+            mgr.append_kv_pages(l, n_keys)
+            info = mgr.get_layer(l)
+            call("genllm_fill_normal_bf16", info.k_pool, pool * PAGE * Hkv * D, 5100 + l, 0, None)
+            call("genllm_fill_normal_bf16", info.v_pool, pool * PAGE * Hkv * D, 5200 + l, 0, None)
+        infos = [mgr.get_layer(l) for l in range(L)]
+        q = torch.empty((Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+        paged.fill_normal_bf16(q, 5300)
+        o = torch.empty_like(q)
+        ws = torch.zeros(paged.decode_workspace_bytes(Hq, Hkv, 1, D, pool), dtype=torch.uint8, device="cuda")
+
+        def launch(i):
+            inf = infos[i % L]
+            paged.paged_decode(q, o, inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, n_pages, n_keys, Hkv,
+                               1.0 / np.sqrt(D), ws)
+
+        avg_us = time_kernels(torch, launch, iters)
+        nbytes = decode_kernel_bytes(n_keys)
+        gbs = nbytes / (avg_us * 1e-6) / 1e9
+        out.append({"n_keys": n_keys, "layers_rotated": L, "avg_launch_us": round(avg_us, 2), "bytes": nbytes,
+                    "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        mgr.close()
+        del ws
     return {"shapes": out}
 
 
@@ -693,7 +736,7 @@ def main():
     if args.only and args.only != "headline":
         fn = {"append": append_cfg2, "prefill": prefill_cfg4, "flash": flash_cfg4, "qwen35": qwen35_d256,
               "longctx": longctx_cfg5, "linear": linear_qkv, "copy": copy_calibration,
-              "prefill_scale": prefill_scale}[args.only]
+              "prefill_scale": prefill_scale, "decode_scale": decode_scale}[args.only]
         print(json.dumps({"only": args.only, **fn(*common)}), flush=True)
         return
 
