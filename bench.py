@@ -713,7 +713,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {args.gpus}); "
-              "multi-GPU sharding of the path is described in DESIGN.md, not run.", file=sys.stderr)
+              "sharding the path over several GPUs is designed, not built or run here.", file=sys.stderr)
         sys.exit(2)
 
     # HBM traffic and kernel-trace durations of the headline kernels: child
