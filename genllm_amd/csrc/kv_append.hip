@@ -14,7 +14,8 @@
 // its first ones.
 //
 // K/q lanes: lane j of a row holds elements 4j + 32t + {0,1,2,3}, t = 0..D/32-1
-// (one 8-byte load per t).  That puts the CPU rms_norm's 32 running sums
+// (one 8-byte load per t; K rows are stored 16 bytes at a time after a swap
+// with lane j ^ 1).  That puts the CPU rms_norm's 32 running sums
 // (element e feeds sum e % 32, fused multiply-adds in increasing e) inside the
 // lanes: lane j owns sums 4j..4j+3 and runs their chains itself, and three
 // 8-lane shuffles reproduce the reference's combine order
@@ -41,7 +42,6 @@
 // within the call, and streaming them past L2 measured 11.6 -> 10.5 us
 // (median C call) at 4096 tokens.
 typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int nt_u32x2 __attribute__((ext_vector_type(2)));
 
 namespace genllm {
 
@@ -59,6 +59,7 @@ struct Append {
     static constexpr int R = D / 32;  // 8-byte chunks per q/k row and lane
     static constexpr int U = D / 64;  // 16-byte chunks per v row and lane
     static_assert(TR >= 1 && 2 * TR <= R, "rotated chunks");
+    static_assert(R % 2 == 0, "K rows are stored as pairs of 8-byte chunks");
 
     // Block id of local page lp (K: which = 0, V: 1): opened by this call ->
     // from the launch arguments, else from the device table.  -1 when the id
@@ -256,10 +257,25 @@ struct Append {
 #pragma unroll
                     for (int c = 0; c < R; ++c) *reinterpret_cast<uint2*>(dst + 4 * j + 32 * c) = x[u][c];
                 } else {  // K page rows: not read again within the call
+                    // 16-byte stores: lanes j and j ^ 1 swap one 8-byte part per
+                    // chunk pair (c, c + 1), so that the even lane holds elements
+                    // 4j .. 4j + 7 of chunk c and the odd one 4(j - 1) .. 4(j - 1) + 7
+                    // of chunk c + 1 (config 2: 7.54-7.58 against 8.18-8.24 us with
+                    // 8-byte stores, A/B on one box; the same swap on the q_out
+                    // stores as well, written with the store kind chosen inside
+                    // the loop or per chunk pair, measured 9.1-19.3 us)
+                    const bool odd = j & 1;
 #pragma unroll
-                    for (int c = 0; c < R; ++c)
-                        __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x2, x[u][c]),
-                                                    reinterpret_cast<nt_u32x2*>(dst + 4 * j + 32 * c));
+                    for (int c = 0; c < R; c += 2) {
+                        const uint2 give = odd ? x[u][c] : x[u][c + 1];
+                        uint2 got;
+                        got.x = __shfl_xor(give.x, 1);
+                        got.y = __shfl_xor(give.y, 1);
+                        const uint2 lo = odd ? got : x[u][c], hi = odd ? x[u][c + 1] : got;
+                        const uint4 v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                        __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x4, v),
+                                                    reinterpret_cast<nt_u32x4*>(dst + 4 * (j & ~1) + 32 * (c + (odd ? 1 : 0))));
+                    }
                 }
             }
         } else {
