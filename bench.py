@@ -9,12 +9,14 @@ Steps rotate over 16 independent layers (~540 MB of touched KV) so the 256 MB
 MALL cannot serve them; each layer's context grows by one token per visit, as
 in a real decode loop, and the algorithmic bytes are counted per step.
 
-value = whole-step algorithmic HBM bytes / step time (GB/s).  roofline = the
-dominant kernel (paged_decode_kernel: split-K attention with the split merge in
-the same launch) timed alone, against 8 TB/s: HIP events around each launch on
-the launch stream, with the GPU kept busy while the host queues the launches
-(so the events see GPU time only, comparable to rocprofv3's kernel duration),
-and the back-to-back rate of the same launches.  The kernel time may not
+value = whole-step algorithmic HBM bytes / GPU time of the op step (GB/s):
+one HIP event pair on the launch stream around the timed steps, queued while a
+bounded spin kernel holds the GPU, so the events see GPU time only; the same
+steps with the host in the loop (wall clock) and the host cost of one op call,
+from Python and from C++ (tests/cpp/test_ops_hip --host-cost), are reported
+beside it under "host".  roofline = the dominant kernels (paged_decode_kernel,
+split-K attention, then paged_decode_merge_kernel, the log-sum-exp merge of the
+splits) timed alone the same way, against 8 TB/s.  The kernel time may not
 exceed the op step's time; the bench exits with an error if it does.  Its HBM
 traffic is measured in the same run: two child rocprofv3 --pmc passes
 (FETCH_SIZE, WRITE_SIZE) over the same launches and a 256 MiB copy that scales
@@ -179,13 +181,30 @@ def headline(args, np, torch, paged, synth, call):
     for i in range(args.warmup):
         op_step(i)
     torch.cuda.synchronize()
-    total_bytes = 0
+    # The op step with the host in the loop: wall clock around the steps as a
+    # caller issuing one step after another sees it (labelled, not the value).
     t0 = time.perf_counter()
     for i in range(args.steps):
-        total_bytes += op_step(args.warmup + i)
+        op_step(args.warmup + i)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    step_s = (t1 - t0) / args.steps
+    host_loop_s = (time.perf_counter() - t0) / args.steps
+    # The op step on the GPU (value, ms_per_step): one HIP event pair on the
+    # launch stream around the timed steps, queued while a bounded spin
+    # kernel holds the GPU, so that it never waits for the host (as the
+    # roofline kernel is timed).  Bytes are those of exactly these steps.
+    base = args.warmup + args.steps
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.4e9 * max(0.002, 3.0 * args.steps * (host_loop_s + 20e-6))))
+    start.record(stream)
+    total_bytes = 0
+    q0 = time.perf_counter()
+    for i in range(args.steps):
+        total_bytes += op_step(base + i)
+    queue_s = (time.perf_counter() - q0) / args.steps
+    stop.record(stream)
+    torch.cuda.synchronize()
+    step_s = 1e-3 * start.elapsed_time(stop) / args.steps
 
     # dominant kernel alone: split-K decode with its in-launch merge, 8193 keys,
     # rotating over the same 16 layers
@@ -201,9 +220,15 @@ def headline(args, np, torch, paged, synth, call):
     kbytes = decode_kernel_bytes(n_keys)
     achieved = kbytes / (k_mean * 1e-6) / 1e9
     res = {
-        "value": round(total_bytes / (t1 - t0) / 1e9, 1),
+        "value": round(total_bytes / (step_s * args.steps) / 1e9, 1),
         "ms_per_step": round(step_s * 1e3, 5),
         "us_per_layer": round(step_s * 1e6, 2),
+        "step_timing": "GPU time of the op step: one HIP event pair on the launch stream around the timed steps, "
+                       "queued behind a spin kernel (the GPU never waits for the host)",
+        "host": {"loop_us_per_step": round(host_loop_s * 1e6, 2),
+                 "loop_note": "wall clock of the same op steps issued one after another from Python, host in the loop",
+                 "python_us_per_call": round(queue_s * 1e6, 2),
+                 "python_note": "host time of one op call from Python (asserts, ctypes, C bookkeeping, two launches)"},
         "config": {"workload": "BASELINE config 3: Qwen3-4B-shape paged decode, batch 1, 8K context, "
                                "append 1 token then attend (op genllm_paged_attention)",
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context_start": n0 + 1,
@@ -664,6 +689,24 @@ def measure_counters():
     return res, "measured in this run"
 
 
+def cpp_host_cost(calls=200):
+    """Host cost of one PAGED_ATTN dispatch measured from C++: the operator
+    test binary's --host-cost mode (calls back to back through
+    kernel::dispatch at config 3's shape, no synchronisation), run as a child
+    process.  Returns (dict or None, note)."""
+    exe = os.path.join(ROOT, "tests", "cpp", "test_ops_hip")
+    if not os.access(exe, os.X_OK):
+        return None, "skipped: tests/cpp/test_ops_hip not built"
+    try:
+        r = subprocess.run([exe, "--host-cost", str(calls)], capture_output=True, text=True, timeout=120)
+    except subprocess.TimeoutExpired:
+        return None, "timed out"
+    for line in r.stdout.splitlines():
+        if line.startswith("{") and "host_us_per_call" in line:
+            return json.loads(line), "measured in this run"
+    return None, f"no result (rc {r.returncode})"
+
+
 def cpu_baseline(mgr, np, paged, synth, args, seed):
     """The oracle (oracle/, single thread) on the headline step, on inputs
     copied back from layer 0 of the GPU run: same pools, same allocator state,
@@ -722,6 +765,10 @@ def main():
     if not args.only and not args.no_traffic:
         traffic, traffic_note = measure_counters()
 
+    cpp_host, cpp_host_note = (None, "skipped (--only)")
+    if not args.only:
+        cpp_host, cpp_host_note = cpp_host_cost()
+
     import numpy as np
     import torch
 
@@ -758,7 +805,12 @@ def main():
         "us_per_layer": head["us_per_layer"],
         "device": torch.cuda.get_device_name(0),
         "roofline": head["roofline"],
+        "step_timing": head["step_timing"],
+        "host": head["host"],
     }
+    result["host"]["cpp_us_per_call"] = cpp_host["host_us_per_call"] if cpp_host else None
+    result["host"]["cpp_note"] = ("host time of one PAGED_ATTN dispatch through kernel::dispatch, from C++ "
+                                  "(tests/cpp/test_ops_hip --host-cost): " + cpp_host_note)
     if traffic:
         result["roofline"]["traffic"] = traffic["bytes"]
         result["roofline"]["traffic_x_algorithmic"] = round(traffic["bytes"] / head["roofline"]["bytes_per_launch"],

@@ -112,6 +112,9 @@ constexpr int kDecodeMaxKvHeads = int(kDecodeCounterBytes / sizeof(int32_t));
 // must be zero before the first step.
 constexpr int kStepPos = 0, kStepLimit = 1, kStepArrivals = 2, kStepError = 3, kStepInts = 4;
 size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages);
+// Decode merge forms (genllm_decode_tuning)
+constexpr int kDecodeMergeKernel = 0, kDecodeMergeFused = 1;
+int set_decode_tuning(int pages_per_split, int merge);
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws);
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream);
 int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream);

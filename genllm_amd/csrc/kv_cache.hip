@@ -11,6 +11,7 @@
 //   * a pool without free pages is an error that leaves the layer unchanged
 //     (the reference breaks out of the loop but still advances num_cached).
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdint>
 #include <cstring>
@@ -36,16 +37,18 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 int device_cu_count() {
-    static std::mutex mu;
-    static std::map<int, int> cache;
+    // per device, resolved once (a decode call reads one atomic, no lock)
+    static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 256;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(dev);
-    if (it != cache.end()) return it->second;
-    int n = 0;
+    if (dev < 0 || dev >= 64) {
+        int n = 0;
+        return hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
     return n;
 }
 
@@ -817,9 +820,9 @@ extern "C" int genllm_paged_attention_step(genllm_kv* kv, int32_t layer, const v
     if (int rc = op_params(*s, q, k, v, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads, n_kv_groups, scale,
                            causal, window_end, p))
         return rc;
+    p.step = s->d_step;
     if (int rc = prepare_attention(p, head_dim, kv)) return rc;
     fuse_append(p, *s, k, v, seq_len, head_dim, 0);
-    p.step = s->d_step;
     return launch_attention(p, head_dim, as_stream(stream));
 }
 
@@ -1043,6 +1046,10 @@ extern "C" int genllm_kv_scatter(const void* k, int64_t k_tok_stride, int64_t k_
     ap.k_ids = const_cast<int32_t*>(k_ids);
     ap.v_ids = const_cast<int32_t*>(v_ids);
     return launch_kv_append(ap, head_dim, as_stream(stream));
+}
+
+extern "C" int genllm_decode_tuning(int32_t pages_per_split, int32_t merge) {
+    return set_decode_tuning(pages_per_split, merge);
 }
 
 extern "C" size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int32_t seq_len,

@@ -42,6 +42,7 @@
 // the output directly.  (A single launch in which the last workgroup merges
 // needs agent-scope fences -- an L2 write-back and invalidate per workgroup on
 // gfx950 -- and measured slower.)
+#include <atomic>
 #include <cfloat>
 #include <string>
 
@@ -624,15 +625,8 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
                        int64_t(h) * ns * rows + ri;
     const float* po = p.partial + (int64_t(h) * ns * rows + ri) * D + d0 + PL * lane;
     const int64_t sstride = int64_t(rows) * D;  // floats between splits
-    auto load_o = [&](int s2, float (&o)[PL]) {
-        if constexpr (PL == 2) {
-            const float2 v = *reinterpret_cast<const float2*>(po + s2 * sstride);
-            o[0] = v.x;
-            o[1] = v.y;
-        } else {
-            o[0] = po[s2 * sstride];
-        }
-    };
+    static_assert(PL == 1, "merge: one dim per lane");
+    auto load_o = [&](int s2, float (&o)[PL]) { o[0] = po[s2 * sstride]; };
 
     float mw = -INFINITY, lw = 0.0f, ow[PL];
 #pragma unroll
@@ -693,10 +687,7 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
         const float inv = 1.0f / L;
         uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride +
                          d0 + PL * lane;
-        if constexpr (PL == 2)
-            *reinterpret_cast<uint32_t*>(orow) = pack2(f32_to_bf16_ref(O[0] * inv), f32_to_bf16_ref(O[1] * inv));
-        else
-            *orow = uint16_t(f32_to_bf16_ref(O[0] * inv));
+        *orow = uint16_t(f32_to_bf16_ref(O[0] * inv));
     }
 }
 
@@ -709,31 +700,54 @@ size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages) {
     return kDecodeCounterBytes + size_t(Hkv) * splits * rows * (D + 2) * sizeof(float);
 }
 
-// The split merge runs in a second kernel unless GENLLM_DECODE_MERGE=fused
-// asks for the single-launch form (the last workgroup of each kv head to
-// finish merges it).  Measured at config 3 (MI355X, 400 back-to-back launches
+// Decode settings, process-wide: initialised once from the environment
+// (GENLLM_DECODE_PPS, GENLLM_DECODE_WG_PER_CU, GENLLM_DECODE_MERGE = kernel |
+// fused) and changed only through genllm_decode_tuning, so a decode call
+// reads no environment.  The split merge runs in a second kernel (default)
+// or, fused, in the split kernel: the last split workgroup of each kv head to
+// finish merges it.  Measured at config 3 (MI355X, 400 back-to-back launches
 // over 16 rotating layers): two kernels 12.7 us per decode (split 10.3 us +
-// merge 3.7 us in the kernel trace), single launch 14.6 us (14.45 us kernel):
-// the last workgroup's serial tail -- coherent stores completing, the arrival
-// count, then coherent loads of every partial -- costs more than the second
-// launch.
-static bool merge_in_split_kernel() {
-    const char* e = getenv("GENLLM_DECODE_MERGE");
-    return e && std::string(e) == "fused";
+// merge 3.7 us in the kernel trace), single launch 14.6 us: the last
+// workgroup's serial tail -- coherent stores completing, the arrival count,
+// then coherent loads of every partial -- costs more than the second launch.
+namespace {
+struct DecodeSettings {
+    std::atomic<int> pps{0};          // > 0: forced pages per split
+    std::atomic<double> wg_per_cu{1.0};
+    std::atomic<int> merge{kDecodeMergeKernel};
+    DecodeSettings() {
+        if (const char* e = getenv("GENLLM_DECODE_PPS")) pps = atoi(e);
+        if (const char* e = getenv("GENLLM_DECODE_WG_PER_CU")) wg_per_cu = atof(e);
+        if (const char* e = getenv("GENLLM_DECODE_MERGE")) {
+            const std::string m(e);
+            merge = m == "fused" ? kDecodeMergeFused : kDecodeMergeKernel;
+        }
+    }
+};
+DecodeSettings& decode_settings() {
+    static DecodeSettings s;
+    return s;
+}
+}  // namespace
+
+int set_decode_tuning(int pages_per_split, int merge) {
+    if (merge != kDecodeMergeKernel && merge != kDecodeMergeFused)
+        return fail(GENLLM_ERR_INVALID, "decode tuning: merge must be 0 (merge kernel) or 1 (fused)");
+    decode_settings().pps = std::max(pages_per_split, 0);
+    decode_settings().merge = merge;
+    return GENLLM_OK;
 }
 
-// Pages per split: about GENLLM_DECODE_WG_PER_CU (default 1) workgroups per CU
-// over all kv heads, at most 256 splits.  GENLLM_DECODE_PPS forces the value
-// (tuning and tests).
+// Pages per split: about wg_per_cu (default 1) workgroups per CU over all kv
+// heads, at most 256 splits (a forced value, genllm_decode_tuning, wins).
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
     if (p.G * p.S > kRows) return fail(GENLLM_ERR_INVALID, "paged decode: seq_len * groups must be <= 16");
+    DecodeSettings& cfg = decode_settings();
     p.n_chunks = 1;
-    int pps = 0;
-    if (const char* e = getenv("GENLLM_DECODE_PPS")) pps = atoi(e);
+    int pps = cfg.pps.load(std::memory_order_relaxed);
+    const int cus = device_cu_count();
     if (pps <= 0) {
-        double per_cu = 1.0;
-        if (const char* e = getenv("GENLLM_DECODE_WG_PER_CU")) per_cu = atof(e);
-        const int64_t target = std::max<int64_t>(1, int64_t(per_cu * device_cu_count()));
+        const int64_t target = std::max<int64_t>(1, int64_t(cfg.wg_per_cu.load(std::memory_order_relaxed) * cus));
         pps = int((int64_t(p.n_pages) * p.Hkv + target - 1) / target);
         if (pps < 2) pps = 2;
     }
@@ -752,7 +766,7 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
             return fail(GENLLM_ERR_INVALID, "paged decode: workspace too small (need " + std::to_string(need) +
                                                 " bytes, have " + std::to_string(ws_bytes) + ")");
         p.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kDecodeCounterBytes);
-        if (merge_in_split_kernel()) p.counters = static_cast<int32_t*>(ws);
+        if (cfg.merge.load(std::memory_order_relaxed) == kDecodeMergeFused) p.counters = static_cast<int32_t*>(ws);
     }
     return GENLLM_OK;
 }

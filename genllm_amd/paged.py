@@ -11,6 +11,7 @@ computation runs in libgenllm_hip.so.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 
 import numpy as np
@@ -315,6 +316,25 @@ def paged_decode(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: i
     call("genllm_paged_decode", _ptr(q), qs[0], qs[1], _ptr(out), os_[0], os_[1], _ptr(k_pool), _ptr(v_pool),
          _ptr(k_ids), _ptr(v_ids), n_pages, n_cached, S, Hq, n_kv_heads, D, float(scale), int(causal),
          _ptr(workspace), ws_bytes, _stream(stream))
+
+
+DECODE_MERGE = {"kernel": 0, "fused": 1}
+
+
+def decode_tuning(pages_per_split: int = 0, merge: str = "kernel"):
+    """genllm_decode_tuning: process-wide decode split size (0 = automatic)
+    and merge form ("kernel" or "fused") for later decode calls."""
+    call("genllm_decode_tuning", int(pages_per_split), DECODE_MERGE[merge])
+
+
+@contextlib.contextmanager
+def decode_tuned(pages_per_split: int = 0, merge: str = "kernel"):
+    """decode_tuning for the duration of a with-block, then the defaults."""
+    decode_tuning(pages_per_split, merge)
+    try:
+        yield
+    finally:
+        decode_tuning(0, "kernel")
 
 
 def paged_decode_noalloc(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: int, n_kv_heads: int,

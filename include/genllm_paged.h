@@ -242,15 +242,25 @@ size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads
 /* The attention loop of PagedAttentionImpl (attention.cpp:148-215) for short
  * query chunks (seq_len * n_q_heads / n_kv_heads <= 16 rows per kv head):
  * split-K over pages, GQA rows packed per kv head, then a log-sum-exp merge of
- * the splits by a second kernel on the same stream (or, with
- * GENLLM_DECODE_MERGE=fused, in the same launch by the last split of each kv
- * head to finish).  q/out rows addressed as base + h*head_stride + s*tok_stride
+ * the splits by a second kernel on the same stream (genllm_decode_tuning
+ * selects a single-launch form).  q/out rows addressed as base + h*head_stride + s*tok_stride
  * (elements).  n_cached = total_cached; query s sits at n_cached - seq_len + s. */
 int genllm_paged_decode(const void *q, int64_t q_head_stride, int64_t q_tok_stride, void *out,
                         int64_t o_head_stride, int64_t o_tok_stride, const void *k_pool, const void *v_pool,
                         const int32_t *k_ids, const int32_t *v_ids, int32_t n_pages, int32_t n_cached,
                         int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
                         int32_t causal, void *workspace, size_t workspace_bytes, void *stream);
+
+/* No counterpart in the reference: a tuning and test hook for the decode
+ * kernels of this library (genllm_paged_decode, _noalloc, the op and its
+ * device-position steps), process-wide, for later calls.  pages_per_split > 0
+ * forces the split size (0: automatic, about one workgroup per CU).  merge:
+ * 0 = a merge kernel after the split kernel (default), 1 = the last split
+ * workgroup of each kv head to finish merges it in the same launch.  The
+ * initial values come from GENLLM_DECODE_PPS and GENLLM_DECODE_MERGE
+ * (kernel | fused), read once.  Returns GENLLM_ERR_INVALID for another merge
+ * value. */
+int genllm_decode_tuning(int32_t pages_per_split, int32_t merge);
 
 /* No counterpart in the reference: genllm_paged_decode for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

@@ -1,14 +1,16 @@
 // test_ops_hip.cpp -- the HIP backend driven through the reference's operator
 // interface (Tensor nodes -> kernel::dispatch -> ops::*Impl<Device::HIP>), in
-// the style of the reference's tests/test_page_attention.cpp and
-// tests/test_ops_cpu.cpp.  Results are checked against the CPU restatement in
+// the spirit of the reference's tests/test_page_attention.cpp and
+// tests/test_ops_cpu.cpp (same sequences, checked with check.hpp).  Results are checked against the CPU restatement in
 // oracle/ (liboracle.so): page tables and K/V pages bit-exact, RMSNorm /
 // RoPE / rope tables bit-exact, attention within max-abs <= 2^-7 * max|ref|
 // and relative L2 <= 1e-2.  Needs one GPU.
 #include <hip/hip_runtime_api.h>
 
+#include <chrono>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -20,7 +22,7 @@
 #include "genllm/tensor.hpp"
 #include "genllm_paged.h"
 #include "oracle.h"
-#include "test_utils.hpp"
+#include "check.hpp"
 
 namespace {
 
@@ -87,49 +89,46 @@ bool attn_close(const std::vector<uint16_t>& got, const std::vector<uint16_t>& w
 }
 
 // ---------------------------------------------------------------- enums
-bool test_device_enum() {
+void test_device_enum(check::Context& c) {
     // tests/test_tensor.cpp:72-76, plus the HIP value
-    ASSERT(static_cast<int>(Device::CPU) == 0, "cpu=0");
-    ASSERT(static_cast<int>(Device::CUDA) == 1, "cuda=1");
-    ASSERT(static_cast<int>(Device::HIP) == 2, "hip=2");
-    ASSERT(static_cast<int>(Device::VULKAN) == 4, "vulkan=4");
-    ASSERT(static_cast<int>(OperationType::OP_TYPE_PAGED_ATTN) == 24, "paged attn op id");
-    ASSERT(static_cast<int>(DataType::GGML_TYPE_BF16) == 30, "bf16 id");
-    return true;
+    CHECK_TRUE(c, static_cast<int>(Device::CPU) == 0, "cpu=0");
+    CHECK_TRUE(c, static_cast<int>(Device::CUDA) == 1, "cuda=1");
+    CHECK_TRUE(c, static_cast<int>(Device::HIP) == 2, "hip=2");
+    CHECK_TRUE(c, static_cast<int>(Device::VULKAN) == 4, "vulkan=4");
+    CHECK_TRUE(c, static_cast<int>(OperationType::OP_TYPE_PAGED_ATTN) == 24, "paged attn op id");
+    CHECK_TRUE(c, static_cast<int>(DataType::GGML_TYPE_BF16) == 30, "bf16 id");
 }
 
 // ---------------------------------------------- tests/test_page_attention.cpp
-bool test_block_pool_alloc_free() {
+void test_block_pool_alloc_free(check::Context& c) {
     PagedAttentionManager mgr(0, 64 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
     mgr.reserve_layer(0, 100);
     BlockPool pool = mgr.get_layer(0).k_pool;
-    ASSERT(pool.num_blocks() == 0, "initially 0 blocks");
-    ASSERT(pool.num_free() == 0, "initially 0 free");
+    CHECK_TRUE(c, pool.num_blocks() == 0, "initially 0 blocks");
+    CHECK_TRUE(c, pool.num_free() == 0, "initially 0 free");
     const int32_t id = pool.alloc();
-    ASSERT(id == 0, "first alloc returns 0");
-    ASSERT(pool.num_blocks() == 1, "1 block after alloc");
-    ASSERT(pool.alloc() == 1, "second alloc returns 1");
+    CHECK_TRUE(c, id == 0, "first alloc returns 0");
+    CHECK_TRUE(c, pool.num_blocks() == 1, "1 block after alloc");
+    CHECK_TRUE(c, pool.alloc() == 1, "second alloc returns 1");
     pool.free(id);
-    ASSERT(pool.num_free() == 1, "1 free after free");
-    ASSERT(pool.alloc() == id, "reuse freed block");
-    ASSERT(pool.num_free() == 0, "0 free after re-alloc");
-    ASSERT(pool.block_data(1) == static_cast<char*>(pool.block_data(0)) + 16 * 8 * 128 * 2, "block stride");
-    ASSERT(pool.block_data(2) == nullptr, "no data past num_blocks");
-    return true;
+    CHECK_TRUE(c, pool.num_free() == 1, "1 free after free");
+    CHECK_TRUE(c, pool.alloc() == id, "reuse freed block");
+    CHECK_TRUE(c, pool.num_free() == 0, "0 free after re-alloc");
+    CHECK_TRUE(c, pool.block_data(1) == static_cast<char*>(pool.block_data(0)) + 16 * 8 * 128 * 2, "block stride");
+    CHECK_TRUE(c, pool.block_data(2) == nullptr, "no data past num_blocks");
 }
 
-bool test_block_pool_many_allocs() {
+void test_block_pool_many_allocs(check::Context& c) {
     PagedAttentionManager mgr(0, 8 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
     mgr.reserve_layer(0, 10);
     BlockPool pool = mgr.get_layer(0).v_pool;
-    for (int i = 0; i < 10; i++) ASSERT(pool.alloc() >= 0, "alloc within capacity");
-    ASSERT(pool.alloc() == -1, "beyond capacity returns -1");
-    return true;
+    for (int i = 0; i < 10; i++) CHECK_TRUE(c, pool.alloc() >= 0, "alloc within capacity");
+    CHECK_TRUE(c, pool.alloc() == -1, "beyond capacity returns -1");
 }
 
-bool test_block_pool_reset() {
+void test_block_pool_reset(check::Context& c) {
     PagedAttentionManager mgr(0, 8 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
     mgr.reserve_layer(0, 10);
@@ -138,49 +137,47 @@ bool test_block_pool_reset() {
     (void)pool.alloc();
     (void)pool.alloc();
     mgr.reset();
-    ASSERT(pool.num_blocks() == 3, "reset keeps num_blocks");
-    ASSERT(pool.num_free() == 3, "reset adds all back to free");
-    ASSERT(pool.alloc() == 2, "free list [0,1,2] pops 2");
-    return true;
+    CHECK_TRUE(c, pool.num_blocks() == 3, "reset keeps num_blocks");
+    CHECK_TRUE(c, pool.num_free() == 3, "reset adds all back to free");
+    CHECK_TRUE(c, pool.alloc() == 2, "free list [0,1,2] pops 2");
 }
 
-bool test_page_table_append_kv() {
+void test_page_table_append_kv(check::Context& c) {
     PagedAttentionManager mgr(0, 1 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
     // held across the appends, as test_page_attention.cpp:53-61 holds it
     auto& layer = mgr.get_layer(0);
-    ASSERT(layer.active, "layer active");
-    ASSERT(layer.num_cached == 0, "initially 0 cached");
+    CHECK_TRUE(c, layer.active, "layer active");
+    CHECK_TRUE(c, layer.num_cached == 0, "initially 0 cached");
     mgr.append_kv_pages(0, 1);
-    ASSERT(layer.num_cached == 1, "1 token cached");
+    CHECK_TRUE(c, layer.num_cached == 1, "1 token cached");
     mgr.append_kv_pages(0, 31);
-    ASSERT(layer.num_cached == 32, "32 tokens cached");
-    ASSERT(layer.page_table.size() == 2, "2 pages (16+16)");
-    ASSERT(&mgr.get_layer(0) == &layer, "one view per layer");
+    CHECK_TRUE(c, layer.num_cached == 32, "32 tokens cached");
+    CHECK_TRUE(c, layer.page_table.size() == 2, "2 pages (16+16)");
+    CHECK_TRUE(c, &mgr.get_layer(0) == &layer, "one view per layer");
     mgr.reset();
-    ASSERT(layer.num_cached == 0 && layer.page_table.empty(), "reset shows in the view");
-    return true;
+    CHECK_TRUE(c, layer.num_cached == 0 && layer.page_table.empty(), "reset shows in the view");
 }
 
 // get_layer's reference is writable, as the reference's is: an in-place edit
 // of page_table reaches the native table before the next call on the layer.
-bool test_get_layer_edit_in_place() {
+void test_get_layer_edit_in_place(check::Context& c) {
     PagedAttentionManager mgr(0, 4 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_BF16);
     mgr.reserve_layer(0, 8);
     auto& layer = mgr.get_layer(0);
     mgr.append_kv_pages(0, 32);
-    ASSERT(layer.page_table.size() == 2, "2 pages");
+    CHECK_TRUE(c, layer.page_table.size() == 2, "2 pages");
     const PageEntry p0 = layer.page_table[0], p1 = layer.page_table[1];
     std::swap(layer.page_table[0], layer.page_table[1]);  // e.g. a permuted table, set in place
     mgr.append_kv_pages(0, 1);                           // commits the edit, then opens page 2
-    ASSERT(layer.num_cached == 33 && layer.page_table.size() == 3, "append after the edit");
-    ASSERT(layer.page_table[0].k_block_id == p1.k_block_id && layer.page_table[1].k_block_id == p0.k_block_id,
+    CHECK_TRUE(c, layer.num_cached == 33 && layer.page_table.size() == 3, "append after the edit");
+    CHECK_TRUE(c, layer.page_table[0].k_block_id == p1.k_block_id && layer.page_table[1].k_block_id == p0.k_block_id,
            "edit kept");
     std::vector<int32_t> k(3), v(3);
     int32_t n = 0;
-    ASSERT(genllm_kv_page_table(mgr.handle(), 0, k.data(), v.data(), 3, &n) == 0 && n == 3, "native table");
-    ASSERT(k[0] == p1.k_block_id && v[0] == p1.v_block_id && k[1] == p0.k_block_id, "native table holds the edit");
+    CHECK_TRUE(c, genllm_kv_page_table(mgr.handle(), 0, k.data(), v.data(), 3, &n) == 0 && n == 3, "native table");
+    CHECK_TRUE(c, k[0] == p1.k_block_id && v[0] == p1.v_block_id && k[1] == p0.k_block_id, "native table holds the edit");
     layer.page_table[0].k_block_id = 1000;  // not a block the pool handed out
     bool threw = false;
     try {
@@ -188,35 +185,33 @@ bool test_get_layer_edit_in_place() {
     } catch (const std::runtime_error&) {
         threw = true;
     }
-    ASSERT(threw, "an invalid edit is refused at commit");
+    CHECK_TRUE(c, threw, "an invalid edit is refused at commit");
     layer.page_table[0].k_block_id = p1.k_block_id;
     mgr.append_kv_pages(0, 1);
-    ASSERT(layer.num_cached == 34, "usable again once the edit is valid");
-    return true;
+    CHECK_TRUE(c, layer.num_cached == 34, "usable again once the edit is valid");
 }
 
-bool test_page_table_multi_layer() {
+void test_page_table_multi_layer(check::Context& c) {
     PagedAttentionManager mgr(0, 1 << 20);
     mgr.init_layer(0, 8, 128, DataType::GGML_TYPE_F16);
     mgr.init_layer(1, 4, 64, DataType::GGML_TYPE_F32);
-    ASSERT(mgr.is_active(0), "layer 0 active");
-    ASSERT(mgr.is_active(1), "layer 1 active");
-    ASSERT(!mgr.is_active(2), "layer 2 not active");
+    CHECK_TRUE(c, mgr.is_active(0), "layer 0 active");
+    CHECK_TRUE(c, mgr.is_active(1), "layer 1 active");
+    CHECK_TRUE(c, !mgr.is_active(2), "layer 2 not active");
     mgr.append_kv_pages(0, 5);
     mgr.append_kv_pages(1, 20);
-    ASSERT(mgr.get_layer(0).num_cached == 5, "layer0 cached 5");
-    ASSERT(mgr.get_layer(1).num_cached == 20, "layer1 cached 20");
+    CHECK_TRUE(c, mgr.get_layer(0).num_cached == 5, "layer0 cached 5");
+    CHECK_TRUE(c, mgr.get_layer(1).num_cached == 20, "layer1 cached 20");
     mgr.reset();
-    ASSERT(mgr.get_layer(0).num_cached == 0, "after reset layer0 = 0");
-    ASSERT(mgr.get_layer(1).page_table.empty(), "after reset page_table empty");
-    return true;
+    CHECK_TRUE(c, mgr.get_layer(0).num_cached == 0, "after reset layer0 = 0");
+    CHECK_TRUE(c, mgr.get_layer(1).page_table.empty(), "after reset page_table empty");
 }
 
 // ------------------------------------------- scheduler rules and the switch
-bool test_kv_cache_per_layer_switch() {
-    ASSERT(attention_op_type(0) == OperationType::OP_TYPE_FLASH_ATTN, "0 -> flash attention");
-    ASSERT(attention_op_type(1) == OperationType::OP_TYPE_PAGED_ATTN, "1 -> paged attention");
-    ASSERT(attention_op_type(4) == OperationType::OP_TYPE_PAGED_ATTN, ">1 -> paged attention");
+void test_kv_cache_per_layer_switch(check::Context& c) {
+    CHECK_TRUE(c, attention_op_type(0) == OperationType::OP_TYPE_FLASH_ATTN, "0 -> flash attention");
+    CHECK_TRUE(c, attention_op_type(1) == OperationType::OP_TYPE_PAGED_ATTN, "1 -> paged attention");
+    CHECK_TRUE(c, attention_op_type(4) == OperationType::OP_TYPE_PAGED_ATTN, ">1 -> paged attention");
     Tensor k = make_tensor(nullptr, {1, 8, 1, 128});
     Tensor paged = make_tensor(nullptr, {1, 32, 1, 128});
     paged.op_type = OperationType::OP_TYPE_PAGED_ATTN;
@@ -226,16 +221,15 @@ bool test_kv_cache_per_layer_switch() {
     flash.op_type = OperationType::OP_TYPE_FLASH_ATTN;
     flash.layer_id = 1;
     // scheduler.cpp:363-372: 2 * ceil(max_seq/16) * 16 * Hkv * D * elem
-    ASSERT(kv_cache_bytes({&paged}, Device::HIP, 300, 1.0f) == size_t(2) * 19 * 16 * 8 * 128 * 2, "paged sizing");
-    ASSERT(kv_cache_bytes({&flash}, Device::HIP, 300, 1.0f) == 0, "flash attention owns no pages");
-    ASSERT(kv_cache_bytes({&paged}, Device::CPU, 300, 1.0f) == 0, "other device not counted");
-    return true;
+    CHECK_TRUE(c, kv_cache_bytes({&paged}, Device::HIP, 300, 1.0f) == size_t(2) * 19 * 16 * 8 * 128 * 2, "paged sizing");
+    CHECK_TRUE(c, kv_cache_bytes({&flash}, Device::HIP, 300, 1.0f) == 0, "flash attention owns no pages");
+    CHECK_TRUE(c, kv_cache_bytes({&paged}, Device::CPU, 300, 1.0f) == 0, "other device not counted");
 }
 
 // ------------------------------------- the op through the executor's switch
 // A two-layer graph of PAGED_ATTN nodes: prefill chunk of `s0` tokens, then
 // `steps` decode tokens, every call checked against or_paged_attention.
-bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t seed) {
+void run_paged_graph(check::Context& c, int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t seed) {
     const int32_t D = 128, G = Hq / Hkv, max_seq = 256, L = 2;
     const float scale = 1.0f / std::sqrt(float(D));
     MemoryManager mm;
@@ -275,7 +269,7 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
             out.layer_id = l;
             out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
             out.op_params = {float(D), scale, 1.0f, float(G)};
-            ASSERT(kernel::dispatch(&out, 0), "executor dispatches PAGED_ATTN");
+            CHECK_TRUE(c, kernel::dispatch(&out, 0), "executor dispatches PAGED_ATTN");
             std::vector<uint16_t> want(size_t(Hq) * S * D);
             or_paged_attention(ref, l, hq.data(), hk.data(), hv.data(), want.data(), 1, Hq, S, D, Hkv, G, scale, 1);
             char what[96];
@@ -285,11 +279,11 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
             const auto st = pam.get_layer(l);
             std::vector<int32_t> rk(st.page_table.size()), rv(st.page_table.size());
             const int32_t n = or_mgr_get_page_table(ref, l, rk.data(), rv.data(), int32_t(rk.size()));
-            ASSERT(n == int32_t(st.page_table.size()), "page table length");
+            CHECK_TRUE(c, n == int32_t(st.page_table.size()), "page table length");
             for (int32_t i = 0; i < n; ++i)
-                ASSERT(st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
-            ASSERT(st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
-            ASSERT(live.num_cached == or_mgr_num_cached(ref, L - 1), "held view follows the op");
+                CHECK_TRUE(c, st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
+            CHECK_TRUE(c, st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
+            CHECK_TRUE(c, live.num_cached == or_mgr_num_cached(ref, L - 1), "held view follows the op");
         }
     }
     for (int l = 0; l < L && ok; ++l) {
@@ -297,11 +291,11 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
         const size_t pool_elems = size_t(st.k_pool.num_blocks()) * 16 * Hkv * D;
         const auto dk = to_host<uint16_t>(st.k_pool.block_data(0), pool_elems);
         const auto dv = to_host<uint16_t>(st.v_pool.block_data(0), pool_elems);
-        ASSERT(std::memcmp(dk.data(), or_mgr_k_pool(ref, l), pool_elems * 2) == 0, "K pages bit-exact");
-        ASSERT(std::memcmp(dv.data(), or_mgr_v_pool(ref, l), pool_elems * 2) == 0, "V pages bit-exact");
+        CHECK_TRUE(c, std::memcmp(dk.data(), or_mgr_k_pool(ref, l), pool_elems * 2) == 0, "K pages bit-exact");
+        CHECK_TRUE(c, std::memcmp(dv.data(), or_mgr_v_pool(ref, l), pool_elems * 2) == 0, "V pages bit-exact");
     }
     or_mgr_destroy(ref);
-    return ok;
+    CHECK_TRUE(c, ok, "attention within tolerance of the oracle");
 }
 
 // A decode loop captured into one HIP graph (the executor's loop,
@@ -312,12 +306,12 @@ bool run_paged_graph(int32_t Hq, int32_t Hkv, int32_t s0, int steps, uint64_t se
 // RoPE'd q bit-exact and attention within tolerance of the oracle run with
 // host positions; after sync_decode, num_cached and the tables equal the
 // oracle's.
-bool test_decode_step_graph() {
+void test_decode_step_graph(check::Context& c) {
     const int32_t Hq = 32, Hkv = 8, D = 128, G = Hq / Hkv, L = 2, P = 26, steps = 12, max_seq = 128;
     const float scale = 1.0f / std::sqrt(float(D));
     MemoryManager mm;
     hipStream_t s = nullptr;
-    ASSERT(hipStreamCreate(&s) == hipSuccess, "stream");
+    CHECK_TRUE(c, hipStreamCreate(&s) == hipSuccess, "stream");
     std::vector<Tensor> ks(L), sizing(L);
     std::vector<Tensor*> graph;
     for (int l = 0; l < L; ++l) {
@@ -349,11 +343,11 @@ bool test_decode_step_graph() {
         out.layer_id = l;
         out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
         out.op_params = {float(D), scale, 1.0f, float(G)};
-        ASSERT(kernel::dispatch(&out, 0), "prompt");
+        CHECK_TRUE(c, kernel::dispatch(&out, 0), "prompt");
         std::vector<uint16_t> want(size_t(Hq) * P * D);
         or_paged_attention(ref, l, hq.data(), hk.data(), hv.data(), want.data(), 1, Hq, P, D, Hkv, G, scale, 1);
     }
-    ASSERT(hipStreamSynchronize(s) == hipSuccess, "prompt done");
+    CHECK_TRUE(c, hipStreamSynchronize(s) == hipSuccess, "prompt done");
     std::vector<float> hcos(size_t(max_seq) * D), hsin(size_t(max_seq) * D);
     or_rope_cache(hcos.data(), 1e6f, D, max_seq, 1);
     or_rope_cache(hsin.data(), 1e6f, D, max_seq, 0);
@@ -395,11 +389,11 @@ bool test_decode_step_graph() {
     }
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
-    ASSERT(hipStreamBeginCapture(s, hipStreamCaptureModeGlobal) == hipSuccess, "begin capture");
+    CHECK_TRUE(c, hipStreamBeginCapture(s, hipStreamCaptureModeGlobal) == hipSuccess, "begin capture");
     for (int l = 0; l < L; ++l)
         for (Tensor* t : {&ly[l].rq, &ly[l].rk, &ly[l].attn}) kernel::dispatch(t, 0);
-    ASSERT(hipStreamEndCapture(s, &g) == hipSuccess, "end capture");
-    ASSERT(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess, "instantiate");
+    CHECK_TRUE(c, hipStreamEndCapture(s, &g) == hipSuccess, "end capture");
+    CHECK_TRUE(c, hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess, "instantiate");
     for (int step = 0; step < steps && ok; ++step) {
         const int32_t pos = P + step;
         std::vector<std::vector<uint16_t>> hq(L), hk(L), hv(L);
@@ -408,13 +402,13 @@ bool test_decode_step_graph() {
             hk[l] = fill_normal(*ly[l].k, 6000 + 10 * step + l);
             hv[l] = fill_normal(*ly[l].v, 7000 + 10 * step + l);
         }
-        ASSERT(hipGraphLaunch(ge, s) == hipSuccess, "replay");
-        ASSERT(hipStreamSynchronize(s) == hipSuccess, "replay done");
+        CHECK_TRUE(c, hipGraphLaunch(ge, s) == hipSuccess, "replay");
+        CHECK_TRUE(c, hipStreamSynchronize(s) == hipSuccess, "replay done");
         for (int l = 0; l < L && ok; ++l) {
             std::vector<uint16_t> qr(size_t(Hq) * D), kr(size_t(Hkv) * D), want(size_t(Hq) * D);
             or_apply_rope(qr.data(), hq[l].data(), hcos.data(), hsin.data(), Hq, 1, D, pos);
             or_apply_rope(kr.data(), hk[l].data(), hcos.data(), hsin.data(), Hkv, 1, D, pos);
-            ASSERT(to_host<uint16_t>(ly[l].qr->p, qr.size()) == qr, "RoPE'd q at the device position bit-exact");
+            CHECK_TRUE(c, to_host<uint16_t>(ly[l].qr->p, qr.size()) == qr, "RoPE'd q at the device position bit-exact");
             or_paged_attention(ref, l, qr.data(), kr.data(), hv[l].data(), want.data(), 1, Hq, 1, D, Hkv, G, scale, 1);
             char what[80];
             std::snprintf(what, sizeof what, "replay %d layer %d position %d", step, l, pos);
@@ -422,27 +416,27 @@ bool test_decode_step_graph() {
         }
     }
     for (int l = 0; l < L && ok; ++l) {
-        ASSERT(pam.sync_decode(l) == P + steps && !pam.is_staged(l), "num_cached after sync");
+        CHECK_TRUE(c, pam.sync_decode(l) == P + steps && !pam.is_staged(l), "num_cached after sync");
         const auto st = pam.get_layer(l);
         std::vector<int32_t> rk(st.page_table.size()), rv(st.page_table.size());
-        ASSERT(or_mgr_get_page_table(ref, l, rk.data(), rv.data(), int32_t(rk.size())) == int32_t(rk.size()),
+        CHECK_TRUE(c, or_mgr_get_page_table(ref, l, rk.data(), rv.data(), int32_t(rk.size())) == int32_t(rk.size()),
                "page table length");
         for (size_t i = 0; i < rk.size(); ++i)
-            ASSERT(st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
-        ASSERT(st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
+            CHECK_TRUE(c, st.page_table[i].k_block_id == rk[i] && st.page_table[i].v_block_id == rv[i], "page ids");
+        CHECK_TRUE(c, st.num_cached == or_mgr_num_cached(ref, l), "num_cached");
     }
     (void)hipGraphExecDestroy(ge);
     (void)hipGraphDestroy(g);
     mm.set_stream(Device::HIP, 0, nullptr);
     (void)hipStreamDestroy(s);
     or_mgr_destroy(ref);
-    return ok;
+    CHECK_TRUE(c, ok, "attention within tolerance of the oracle");
 }
 
-bool test_paged_attention_qwen06b() { return run_paged_graph(16, 8, 40, 3, 0x5EED0001); }
-bool test_paged_attention_qwen4b() { return run_paged_graph(32, 8, 33, 3, 0x5EED0003); }
+void test_paged_attention_qwen06b(check::Context& c) { run_paged_graph(c, 16, 8, 40, 3, 0x5EED0001); }
+void test_paged_attention_qwen4b(check::Context& c) { run_paged_graph(c, 32, 8, 33, 3, 0x5EED0003); }
 
-bool test_paged_attention_errors() {
+void test_paged_attention_errors(check::Context& c) {
     MemoryManager mm;
     PagedAttentionManager& pam = mm.create_attention_manager(Device::HIP, 0, 8 << 20);
     pam.init_layer(0, 2, 64, DataType::GGML_TYPE_BF16);
@@ -462,13 +456,13 @@ bool test_paged_attention_errors() {
     } catch (const std::runtime_error&) {
         threw = true;
     }
-    ASSERT(threw, "head_dim 64 throws std::runtime_error");
+    CHECK_TRUE(c, threw, "head_dim 64 throws std::runtime_error");
     // inactive layer: silent return, output untouched (attention.cpp:127)
     std::vector<uint16_t> sentinel(4 * 64, 0x7777);
     to_device(o.p, sentinel);
     out.layer_id = 5;
     kernel::paged_attention(&out, 0);
-    ASSERT(to_host<uint16_t>(o.p, sentinel.size()) == sentinel, "inactive layer leaves out untouched");
+    CHECK_TRUE(c, to_host<uint16_t>(o.p, sentinel.size()) == sentinel, "inactive layer leaves out untouched");
     // a CPU node never reaches the HIP backend
     out.device = Device::CPU;
     threw = false;
@@ -477,12 +471,11 @@ bool test_paged_attention_errors() {
     } catch (const std::runtime_error&) {
         threw = true;
     }
-    ASSERT(threw, "dispatchOp throws for a device this library does not serve");
-    return true;
+    CHECK_TRUE(c, threw, "dispatchOp throws for a device this library does not serve");
 }
 
 // ----------------------------------------------- FlashAttention (non-paged)
-bool run_flash(int32_t B, int32_t Hq, int32_t Hkv, int32_t S, bool causal, uint64_t seed) {
+void run_flash(check::Context& c, int32_t B, int32_t Hq, int32_t Hkv, int32_t S, bool causal, uint64_t seed) {
     const int32_t D = 128, G = Hq / Hkv;
     const float scale = 1.0f / std::sqrt(float(D));
     DevBuf q(size_t(B) * Hq * S * D * 2), k(size_t(B) * Hkv * S * D * 2), v(size_t(B) * Hkv * S * D * 2),
@@ -494,20 +487,20 @@ bool run_flash(int32_t B, int32_t Hq, int32_t Hkv, int32_t S, bool causal, uint6
     out.op_type = OperationType::OP_TYPE_FLASH_ATTN;
     out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
     out.op_params = {float(D), scale, causal ? 1.0f : 0.0f, float(G)};
-    ASSERT(kernel::dispatch(&out, 0), "executor dispatches FLASH_ATTN");
+    CHECK_TRUE(c, kernel::dispatch(&out, 0), "executor dispatches FLASH_ATTN");
     std::vector<uint16_t> want(size_t(B) * Hq * S * D);
     or_flash_attention(hq.data(), hk.data(), hv.data(), want.data(), B, Hq, S, Hkv, D, G, scale, causal);
     char what[96];
     std::snprintf(what, sizeof what, "flash B%d Hq%d Hkv%d S%d causal %d", B, Hq, Hkv, S, int(causal));
-    return attn_close(to_host<uint16_t>(o.p, want.size()), want, what);
+    CHECK_TRUE(c, attn_close(to_host<uint16_t>(o.p, want.size()), want, what), "flash attention within tolerance");
 }
 
-bool test_flash_attention_causal() { return run_flash(2, 8, 2, 77, true, 11); }
-bool test_flash_attention_full() { return run_flash(1, 16, 8, 130, false, 12); }
-bool test_flash_attention_one_token() { return run_flash(1, 4, 4, 1, true, 13); }
+void test_flash_attention_causal(check::Context& c) { run_flash(c, 2, 8, 2, 77, true, 11); }
+void test_flash_attention_full(check::Context& c) { run_flash(c, 1, 16, 8, 130, false, 12); }
+void test_flash_attention_one_token(check::Context& c) { run_flash(c, 1, 4, 4, 1, true, 13); }
 
 // ----------------------------------------------------- RMSNorm, RoPE, tables
-bool test_rms_norm_rope_nodes() {
+void test_rms_norm_rope_nodes(check::Context& c) {
     const int32_t H = 5, S = 9, D = 128, max_seq = 64;
     const int64_t start = 7;
     MemoryManager mm;
@@ -533,26 +526,25 @@ bool test_rms_norm_rope_nodes() {
     rope.op_type = OperationType::OP_TYPE_APPLY_ROPE;
     rope.src = {&norm, &cos_t, &sin_t, nullptr, nullptr, nullptr};
     rope.op_params = {float(D), float(D), float(start), 0};
-    for (Tensor* t : {&norm, &cos_t, &sin_t, &rope}) ASSERT(kernel::dispatch(t, 0), "dispatched");
+    for (Tensor* t : {&norm, &cos_t, &sin_t, &rope}) CHECK_TRUE(c, kernel::dispatch(t, 0), "dispatched");
 
     std::vector<float> rc(size_t(max_seq) * D), rs(size_t(max_seq) * D);
     or_rope_cache(rc.data(), 1e6f, D, max_seq, 1);
     or_rope_cache(rs.data(), 1e6f, D, max_seq, 0);
-    ASSERT(to_host<float>(cs.p, rc.size()) == rc, "cos table bit-exact");
-    ASSERT(to_host<float>(sn.p, rs.size()) == rs, "sin table bit-exact");
+    CHECK_TRUE(c, to_host<float>(cs.p, rc.size()) == rc, "cos table bit-exact");
+    CHECK_TRUE(c, to_host<float>(sn.p, rs.size()) == rs, "sin table bit-exact");
     std::vector<uint16_t> yn(hx.size()), yr(hx.size());
     or_rms_norm(yn.data(), hx.data(), gamma.data(), size_t(H) * S, D, 1e-6f);
-    ASSERT(to_host<uint16_t>(y.p, yn.size()) == yn, "rms_norm bit-exact");
+    CHECK_TRUE(c, to_host<uint16_t>(y.p, yn.size()) == yn, "rms_norm bit-exact");
     or_apply_rope(yr.data(), yn.data(), rc.data(), rs.data(), H, S, D, start);
-    ASSERT(to_host<uint16_t>(r.p, yr.size()) == yr, "apply_rope bit-exact");
-    return true;
+    CHECK_TRUE(c, to_host<uint16_t>(r.p, yr.size()) == yr, "apply_rope bit-exact");
 }
 
 // ------------------------------------------------------------------- Linear
 // LINEAR node (linear.cpp:325-345): decode-sized M bit-exact against the
 // oracle's restatement of the reference's summation order; a prefill-sized M
 // through the GEMM path within one bf16 rounding of it.
-bool run_linear(int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_t seed, bool exact) {
+void run_linear(check::Context& c, int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_t seed, bool exact) {
     MemoryManager mm;
     DevBuf x(size_t(M * common * 2)), w(size_t(cols * common * 2)), b(size_t(cols * 2)), o(size_t(M * cols * 2));
     auto hx = fill_normal(x, seed), hw = fill_normal(w, seed + 1), hb = fill_normal(b, seed + 2);
@@ -571,15 +563,15 @@ bool run_linear(int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_
         } catch (const std::runtime_error&) {
             threw = true;
         }
-        ASSERT(threw, "linear GEMM with a bias refuses to run without a reserved op workspace");
+        CHECK_TRUE(c, threw, "linear GEMM with a bias refuses to run without a reserved op workspace");
         mm.reserve_op_workspace(Device::HIP, 0, ws);
     }
-    ASSERT(kernel::dispatch(&out, 0), "executor dispatches LINEAR");
+    CHECK_TRUE(c, kernel::dispatch(&out, 0), "executor dispatches LINEAR");
     std::vector<uint16_t> want(size_t(M * cols));
     or_linear_bf16(want.data(), hx.data(), hw.data(), M, common, cols, with_bias ? hb.data() : nullptr);
     const auto got = to_host<uint16_t>(o.p, want.size());
     if (exact) {
-        ASSERT(got == want, "linear bit-exact against the oracle");
+        CHECK_TRUE(c, got == want, "linear bit-exact against the oracle");
     } else {
         // both sides are one bf16 rounding of an fp32 sum: |got - want| <= one
         // bf16 ulp of the larger plus twice the fp32 accumulation bound
@@ -595,23 +587,76 @@ bool run_linear(int64_t M, int64_t common, int64_t cols, bool with_bias, uint64_
                 const double ulp = std::ldexp(1.0, std::ilogb(std::max(big, 1e-38)) - 7);
                 if (std::abs(a - b) > ulp + 2.0 * double(common) * std::ldexp(1.0, -24) * mag) ++far;
             }
-        ASSERT(far == 0, "linear GEMM within one bf16 rounding + fp32 accumulation error of the oracle");
+        CHECK_TRUE(c, far == 0, "linear GEMM within one bf16 rounding + fp32 accumulation error of the oracle");
     }
-    return true;
 }
 
-bool test_linear_decode() { return run_linear(1, 2560, 1024, false, 31, true) && run_linear(3, 1024, 300, true, 32, true); }
-bool test_linear_prefill() { return run_linear(64, 1024, 512, true, 33, false) && run_linear(64, 1024, 512, false, 34, false); }
+void test_linear_decode(check::Context& c) {
+    run_linear(c, 1, 2560, 1024, false, 31, true);
+    if (c.ok()) run_linear(c, 3, 1024, 300, true, 32, true);
+}
+void test_linear_prefill(check::Context& c) {
+    run_linear(c, 64, 1024, 512, true, 33, false);
+    if (c.ok()) run_linear(c, 64, 1024, 512, false, 34, false);
+}
+
+// Host cost of one PAGED_ATTN dispatch at config 3's shape (Qwen3-4B heads,
+// 8192 cached tokens, one decode token): `calls` dispatches back to back
+// through kernel::dispatch, timed on the host without synchronising while the
+// GPU runs them (host bookkeeping, the split plan and two kernel launches).
+// Prints one JSON line.
+int host_cost(int calls) {
+    const int32_t Hq = 32, Hkv = 8, D = 128, G = Hq / Hkv, cached = 8192;
+    const int32_t max_seq = cached + calls + 64;
+    MemoryManager mm;
+    Tensor kproto = make_tensor(nullptr, {1, Hkv, 1, D});
+    Tensor proto = make_tensor(nullptr, {1, Hq, 1, D});
+    proto.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+    proto.src[1] = &kproto;
+    proto.layer_id = 0;
+    std::vector<Tensor*> graph{&proto};
+    PagedAttentionManager& pam =
+        mm.create_attention_manager(Device::HIP, 0, kv_cache_bytes(graph, Device::HIP, max_seq));
+    initialize_kv_cache(pam, graph, max_seq);
+    pam.append_kv_pages(0, cached);
+    DevBuf q(size_t(Hq) * D * 2), k(size_t(Hkv) * D * 2), v(size_t(Hkv) * D * 2), o(size_t(Hq) * D * 2);
+    fill_normal(q, 1);
+    fill_normal(k, 2);
+    fill_normal(v, 3);
+    Tensor Q = make_tensor(q.p, {1, Hq, 1, D}), K = make_tensor(k.p, {1, Hkv, 1, D}), V = make_tensor(v.p, {1, Hkv, 1, D});
+    Tensor out = make_tensor(o.p, {1, Hq, 1, D});
+    out.op_type = OperationType::OP_TYPE_PAGED_ATTN;
+    out.layer_id = 0;
+    out.src = {&Q, &K, &V, nullptr, nullptr, nullptr};
+    out.op_params = {float(D), 1.0f / std::sqrt(float(D)), 1.0f, float(G)};
+    for (int i = 0; i < 16; ++i)
+        if (!kernel::dispatch(&out, 0)) return 1;
+    if (hipDeviceSynchronize() != hipSuccess) return 1;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < calls; ++i)
+        if (!kernel::dispatch(&out, 0)) return 1;
+    const auto t1 = std::chrono::steady_clock::now();
+    if (hipDeviceSynchronize() != hipSuccess) return 1;
+    if (pam.get_layer(0).num_cached != cached + 16 + calls) {  // every call appended its token
+        std::printf("host cost: the op did not run (num_cached %d)\n", pam.get_layer(0).num_cached);
+        return 1;
+    }
+    const double us = std::chrono::duration<double, std::micro>(t1 - t0).count() / calls;
+    std::printf("{\"host_us_per_call\": %.3f, \"calls\": %d, \"shape\": \"Hq %d, Hkv %d, D %d, %d+ cached\"}\n", us,
+                calls, Hq, Hkv, D, cached);
+    return 0;
+}
 
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
         std::printf("no HIP device\n");
         return 2;
     }
-    return run_tests({
+    if (argc == 3 && std::strcmp(argv[1], "--host-cost") == 0) return host_cost(std::max(1, std::atoi(argv[2])));
+    return check::main({
         {"device enum", test_device_enum},
         {"block_pool alloc/free", test_block_pool_alloc_free},
         {"block_pool many allocs", test_block_pool_many_allocs},
@@ -630,5 +675,5 @@ int main() {
         {"rms_norm / rope_cache / apply_rope nodes", test_rms_norm_rope_nodes},
         {"linear node, decode rows (bit-exact)", test_linear_decode},
         {"linear node, prefill rows (GEMM)", test_linear_prefill},
-    });
+    }, argc, argv);
 }

@@ -2,7 +2,6 @@
 the oracle's PagedAttentionImpl<CPU> attention loop, on identical pools and
 block tables.  Tolerance (bf16 output, fp32 accumulate): max-abs <= 2^-7 *
 max|ref| and rel-L2 <= 1e-2 (helpers.assert_attn_close)."""
-import os
 
 import numpy as np
 import pytest
@@ -53,22 +52,11 @@ class Context:
         n_pages = (self.n_ctx + 15) // 16
         ws = torch.zeros(paged.decode_workspace_bytes(Hq, self.Hkv, S, D, n_pages), dtype=torch.uint8,
                          device="cuda")
-        saved = {k: os.environ.get(k) for k in ("GENLLM_DECODE_PPS", "GENLLM_DECODE_MERGE")}
-        if pps:
-            os.environ["GENLLM_DECODE_PPS"] = str(pps)
-        if merge:
-            os.environ["GENLLM_DECODE_MERGE"] = merge
-        try:
+        with paged.decode_tuned(pps or 0, merge or "kernel"):
             info = self.info
             paged.paged_decode(paged.to_device_bf16(q_bits), out, info.k_pool, info.v_pool, info.k_ids, info.v_ids,
                                n_pages, self.n_ctx, self.Hkv, scale_for(D), ws, causal=causal)
             torch.cuda.synchronize()
-        finally:
-            for k, v in saved.items():
-                if v is None:
-                    os.environ.pop(k, None)
-                else:
-                    os.environ[k] = v
         return paged.to_host_bits(out), ws
 
     def oracle(self, q_bits, causal=True):
@@ -212,4 +200,26 @@ def test_decode_single_launch_merge(orc, Hq, Hkv, D, N, S, pps):
     assert not ws[:1024].any().item(), "arrival counters not back at zero"
     two, _ = ctx.decode(q, pps=pps)
     assert_attn_close(two, ref, "two-kernel merge")
+    ctx.close()
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,N,S,pps", [(32, 8, 128, 8193, 1, None), (32, 8, 128, 32761, 1, None),
+                                            (16, 8, 128, 1000, 8, 3), (8, 2, 256, 8193, 1, None),
+                                            (32, 8, 128, 4100, 1, 64)])
+def test_decode_merge_forms_agree(orc, Hq, Hkv, D, N, S, pps):
+    """The merge kernel (default) and the single-launch merge give the same
+    bits on the same inputs, match the oracle, and leave the arrival counters
+    at zero -- also over several launches in a row on one workspace."""
+    pool = (N + 15) // 16 + 3
+    ctx = Context(orc, Hkv, D, pool, N, 7300 + N + S, nan_tail=True)
+    q = synth.normal_bf16(7400 + N, (Hq, S, D))
+    ref = ctx.oracle(q)
+    outs = {}
+    for merge in ("kernel", "fused", "kernel", "fused"):
+        got, ws = ctx.decode(q, pps=pps, merge=merge)
+        assert_attn_close(got, ref, f"{merge} merge Hq{Hq} Hkv{Hkv} D{D} N{N} S{S}")
+        assert not ws[:1024].any().item(), f"{merge}: arrival counters not back at zero"
+        if merge in outs:
+            assert np.array_equal(outs[merge], got), f"{merge}: repeat differs"
+        outs[merge] = got
     ctx.close()

@@ -255,13 +255,14 @@ def test_step_head_dim_256_across_8192(orc):
     (32, 8, 128, 1, 200, 128, "fused"),  # single-launch merge: no merge kernel either
     (8, 2, 256, 1, 90, 64, None),       # Qwen3.5: RoPE on the first 64 of 256 dims
 ])
-def test_step_variants(orc, monkeypatch, Hq, Hkv, D, S, P, rope_dim, merge):
+def test_step_variants(orc, request, Hq, Hkv, D, S, P, rope_dim, merge):
     """Device-position steps beyond the single-token default plan: the query
     chunk, the split plan, the merge form and the rotary width change, and
     every replay still matches the oracle run with host positions (RoPE'd q
     bit-exact, attention within tolerance, pools bit-exact)."""
     if merge:
-        monkeypatch.setenv("GENLLM_DECODE_MERGE", merge)
+        paged.decode_tuning(0, merge)
+        request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
     G, L, steps, max_seq = Hq // Hkv, 2, 8, 512
     pool = (P + S * steps + 15) // 16 + 2
     st = Stack(orc, L, Hq, Hkv, D, pool=pool, P=P, seed=0x5EED0400 + S + D + P)

@@ -64,10 +64,10 @@ class Cache:
         self.mgr.close()
 
 
-@pytest.mark.parametrize("merge", [None, "fused"])
-def test_noalloc_matches_workspace_entry_point(orc, merge, monkeypatch):
-    if merge:
-        monkeypatch.setenv("GENLLM_DECODE_MERGE", merge)
+@pytest.mark.parametrize("merge", ["kernel", "kernel", "fused"])
+def test_noalloc_matches_workspace_entry_point(orc, merge, request):
+    paged.decode_tuning(0, merge)
+    request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
     # config 3's shape (8193 keys, 32 q / 8 kv heads), then a smaller call on
     # the same scratch: fewer keys, fewer rows
     c = Cache(orc, 8, 128, 600, 8193, 4242)
@@ -86,13 +86,14 @@ def test_noalloc_matches_workspace_entry_point(orc, merge, monkeypatch):
     c2.close()
 
 
-def test_noalloc_refuses_plans_beyond_its_scratch(orc, monkeypatch):
+def test_noalloc_refuses_plans_beyond_its_scratch(orc, request):
     """16 rows per kv head over 8 kv heads at 8193 keys with 3 pages per
     split: 8 x 171 splits x 16 rows x 130 x 4 B = 11.4 MB of partials, more
     than the 4 MiB scratch -- refused with GENLLM_ERR_INVALID, output
     untouched; the next call that fits still matches the workspace entry
     point."""
-    monkeypatch.setenv("GENLLM_DECODE_PPS", "3")
+    paged.decode_tuning(3, "kernel")
+    request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
     c = Cache(orc, 8, 128, 600, 8193, 4246)
     q = paged.to_device_bf16(synth.normal_bf16(4247, (32, 4, 128)))  # G=4, S=4: 16 rows
     out = torch.zeros((32, 4, 128), dtype=torch.bfloat16, device="cuda")
@@ -102,7 +103,7 @@ def test_noalloc_refuses_plans_beyond_its_scratch(orc, monkeypatch):
     assert e.value.code == ERR_INVALID and "scratch" in str(e.value)
     torch.cuda.synchronize()
     assert not out.float().abs().sum().item()
-    monkeypatch.delenv("GENLLM_DECODE_PPS")
+    paged.decode_tuning(0, "kernel")
     q1 = synth.normal_bf16(4248, (32, 1, 128))
     assert np.array_equal(c.run(q1, 8193, noalloc=True), c.run(q1, 8193, noalloc=False))
     c.close()
