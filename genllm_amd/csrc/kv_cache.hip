@@ -429,6 +429,17 @@ extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max
     // the scheduler's sizing, scheduler.cpp:62-79 and 371); the device page
     // table, its pinned staging and the decode workspace are allocated
     // separately, once, here.
+    // The decode workspace grows (a new buffer) only while no layer is staged:
+    // a captured device-position step holds the current buffer's address.
+    // Checked first, so that a refusal changes nothing.
+    const int rows = 16;  // decode kernel limit: (query, q-head) rows per kv head
+    const size_t ws_need = decode_workspace_bytes(rows * s.n_kv_heads, s.n_kv_heads, 1, s.head_dim, max_blocks);
+    if (ws_need > kv->ws_bytes)
+        for (const auto& kvp : kv->layers)
+            if (kvp.second.active && kvp.second.staged)
+                return fail(GENLLM_ERR_INVALID,
+                            "reserve_layer: this layer needs a larger decode workspace, which cannot be replaced "
+                            "while layer " + std::to_string(kvp.first) + " is staged (reserve every layer first)");
     const size_t cursor0 = kv->cursor;
     void *kp, *vp;
     if (int rc = pool_allocate(kv, total, 256, &kp)) return rc;
@@ -448,12 +459,14 @@ extern "C" int genllm_kv_reserve_layer(genllm_kv* kv, int32_t layer, int32_t max
         kv->cursor = cursor0;
         return hip_fail(e, "reserve_layer: page table allocation");
     }
+    if (int rc = reserve_workspace(kv, ws_need)) {  // nothing of this call is kept
+        (void)hipFree(table);
+        (void)hipHostFree(staging);
+        kv->cursor = cursor0;
+        return rc;
+    }
     kv->tables.push_back(table);
     kv->pinned.push_back(staging);
-    const int rows = 16;  // decode kernel limit: (query, q-head) rows per kv head
-    if (int rc = reserve_workspace(
-            kv, decode_workspace_bytes(rows * s.n_kv_heads, s.n_kv_heads, 1, s.head_dim, max_blocks)))
-        return rc;
     s.h_ids = static_cast<int32_t*>(staging);
     s.k_base = static_cast<uint16_t*>(kp);
     s.v_base = static_cast<uint16_t*>(vp);

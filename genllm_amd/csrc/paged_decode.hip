@@ -205,6 +205,7 @@ template <int D>
 struct PageRegs {
     uint4 k[D / 32];       // K^T operand chunks
     uint4 v[4][D / 128];   // V rows of tokens 4g..4g+3, dims 8 n16 + 128 hh
+    int kid, vid;          // the page's block ids (wave-uniform)
 };
 
 // Reads a word of the step control block at the device's coherence point
@@ -258,21 +259,31 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         p.k_ids_w[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
         p.v_ids_w[p.upd.first + threadIdx.x] = p.upd.v[threadIdx.x];
     }
-    int my_kid = 0, my_vid = 0;  // block-table entries of the wave's pages, one per lane
-    if (lane < np_plan) {
-        // (loading both candidates, from the launch arguments and the table,
-        // and selecting the value measured 0.25 us slower at config 3: every
-        // lane then reads the launch arguments)
-        const int pg = begin + wv + W * lane;
-        const int rel = pg - p.upd.first;
-        if (rel >= 0 && rel < p.upd.count) {
-            my_kid = p.upd.k[rel];
-            my_vid = p.upd.v[rel];
-        } else {
-            my_kid = p.k_ids[pg];
-            my_vid = p.v_ids[pg];
+    // Block-table entries of the wave's pages, 64 at a time: lane i holds the
+    // ids of the wave's page 64 b + i of id block b.  The current block is in
+    // my_kid / my_vid, the next one (requested as the wave enters the current
+    // one) in nx_kid / nx_vid, so a split may span any number of pages.
+    // (Loading both candidates, from the launch arguments and the table, and
+    // selecting the value measured 0.25 us slower at config 3: every lane then
+    // reads the launch arguments.)
+    auto fetch_ids = [&](int b, int& kid, int& vid) {
+        kid = vid = 0;
+        const int jj = 64 * b + lane;
+        if (jj < np_plan) {
+            const int pg = begin + wv + W * jj;
+            const int rel = pg - p.upd.first;
+            if (rel >= 0 && rel < p.upd.count) {
+                kid = p.upd.k[rel];
+                vid = p.upd.v[rel];
+            } else {
+                kid = p.k_ids[pg];
+                vid = p.v_ids[pg];
+            }
         }
-    }
+    };
+    int my_kid, my_vid, nx_kid = 0, nx_vid = 0;
+    fetch_ids(0, my_kid, my_vid);
+    if (np_plan > 64) fetch_ids(1, nx_kid, nx_vid);  // wave-uniform
 
     // Cache position: from the launch arguments, or (device-position step)
     // from the control block, where a step that would pass the staged limit
@@ -314,8 +325,8 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     // Token t >= new_from is this call's append: read it from k_new / v_new.
     auto load_page = [&](int j, PageRegs<D>& pr, bool special) {
         const int pg = page_of(j);
-        const uint16_t* kb = p.k_pool + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
-        const uint16_t* vb = p.v_pool + int64_t(__builtin_amdgcn_readlane(my_vid, j)) * p.page_elems;
+        const uint16_t* kb = p.k_pool + int64_t(pr.kid) * p.page_elems;
+        const uint16_t* vb = p.v_pool + int64_t(pr.vid) * p.page_elems;
         if (!special) {
             // buffer loads: scalar page base in the resource (whose size bounds
             // every lane offset), 32-bit lane offset, row offset as immediate
@@ -360,8 +371,8 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     auto store_new = [&](int j, const PageRegs<D>& pr) {
         const int pg = page_of(j);
         if (pg * kPage + kPage <= new_from) return;  // wave-uniform: no new token in this page
-        uint16_t* kb = p.k_pool_w + int64_t(__builtin_amdgcn_readlane(my_kid, j)) * p.page_elems;
-        uint16_t* vb = p.v_pool_w + int64_t(__builtin_amdgcn_readlane(my_vid, j)) * p.page_elems;
+        uint16_t* kb = p.k_pool_w + int64_t(pr.kid) * p.page_elems;
+        uint16_t* vb = p.v_pool_w + int64_t(pr.vid) * p.page_elems;
         const int tk = pg * kPage + n16;
         if (tk >= new_from && tk < n_cached) {
 #pragma unroll
@@ -453,7 +464,16 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         __builtin_amdgcn_wave_barrier();
     };
 
+    // pages are loaded in increasing j, each once: the wave moves to id block
+    // j / 64 when it first loads a page of it
     auto load_any = [&](int j, PageRegs<D>& pr) {
+        if (j > 0 && (j & 63) == 0) {  // wave-uniform
+            my_kid = nx_kid;
+            my_vid = nx_vid;
+            if (j + 64 < np_plan) fetch_ids(j / 64 + 1, nx_kid, nx_vid);
+        }
+        pr.kid = __builtin_amdgcn_readlane(my_kid, j & 63);
+        pr.vid = __builtin_amdgcn_readlane(my_vid, j & 63);
         if (page_of(j) >= special_from)
             load_page(j, pr, true);
         else
@@ -752,7 +772,6 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
         if (pps < 2) pps = 2;
     }
     pps = std::max(pps, (p.n_pages + kMaxSplits - 1) / kMaxSplits);
-    pps = std::min(pps, 64 * kWaves);  // a wave holds the ids of at most 64 pages
     p.pages_per_split = pps;
     p.n_splits = (p.n_pages + pps - 1) / pps;
     p.partial = nullptr;
@@ -806,7 +825,7 @@ int launch_decode_d(const AttnParams& p, hipStream_t stream) {
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (head_dim != 128 && head_dim != 256) return fail(GENLLM_ERR_UNSUPPORTED, "paged decode: head_dim must be 128 or 256");
     if (p.n_pages <= 0) return GENLLM_OK;
-    if (p.n_splits > kMaxSplits || p.pages_per_split > 64 * kWaves || p.G * p.S > kRows)
+    if (p.n_splits > kMaxSplits || p.pages_per_split <= 0 || p.G * p.S > kRows)
         return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
     return head_dim == 128 ? launch_decode_d<128>(p, stream) : launch_decode_d<256>(p, stream);
 }

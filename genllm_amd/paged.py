@@ -310,8 +310,15 @@ def _attn_args(q, out, q_layout):
 
 
 def paged_decode(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: int, n_kv_heads: int,
-                 scale: float, workspace, causal: bool = True, q_layout: str = "head", stream=None):
+                 scale: float, workspace=None, causal: bool = True, q_layout: str = "head", stream=None):
+    """genllm_paged_decode.  workspace: a device buffer of at least
+    decode_workspace_bytes(...) bytes, zero-filled before its first use (its
+    arrival counters must start at zero; every launch leaves them at zero);
+    None allocates a zero-filled one for this call."""
     Hq, S, D, qs, os_ = _attn_args(q, out, q_layout)
+    if workspace is None:
+        workspace = torch.zeros(decode_workspace_bytes(Hq, n_kv_heads, S, D, n_pages), dtype=torch.uint8,
+                                device=q.device)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     call("genllm_paged_decode", _ptr(q), qs[0], qs[1], _ptr(out), os_[0], os_[1], _ptr(k_pool), _ptr(v_pool),
          _ptr(k_ids), _ptr(v_ids), n_pages, n_cached, S, Hq, n_kv_heads, D, float(scale), int(causal),

@@ -230,13 +230,23 @@ class Manager:
     """PagedAttentionManager restated (page_attention.cpp:66-216)."""
 
     def __init__(self, with_pool: bool = True):
+        # the destructor is held by the instance: at interpreter exit the
+        # module's globals (lib) may already be gone when __del__ runs
+        self._destroy = lib().or_mgr_destroy
         self._h = lib().or_mgr_create(int(with_pool))
         self._shapes = {}
 
+    def close(self):
+        h, self._h = getattr(self, "_h", None), None
+        destroy = getattr(self, "_destroy", None)
+        if h and destroy is not None:
+            destroy(h)
+
     def __del__(self):
-        if getattr(self, "_h", None):
-            lib().or_mgr_destroy(self._h)
-            self._h = None
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: nothing left to release
+            pass
 
     def init_layer(self, layer, n_kv_heads, head_dim, dtype=BF16):
         self._shapes[layer] = (n_kv_heads, head_dim)

@@ -223,3 +223,19 @@ def test_decode_merge_forms_agree(orc, Hq, Hkv, D, N, S, pps):
             assert np.array_equal(outs[merge], got), f"{merge}: repeat differs"
         outs[merge] = got
     ctx.close()
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,N,pps", [(32, 8, 128, 8193, 513), (32, 8, 128, 8193, 300),
+                                          (16, 8, 128, 20000, 1250), (8, 2, 256, 8193, 300)])
+def test_decode_splits_spanning_several_id_blocks(orc, Hq, Hkv, D, N, pps):
+    """Splits longer than 64 pages per wave: a wave moves through blocks of 64
+    page ids (the next block requested as it enters the current one), so a
+    split may span any number of pages -- one split of all 513 pages, two of
+    300, one of 1250 (5 id blocks per wave) and the head_dim 256 form (two
+    pages in flight), against the oracle."""
+    pool = (N + 15) // 16 + 5
+    ctx = Context(orc, Hkv, D, pool, N, 7600 + N + pps, nan_tail=True)
+    q = synth.normal_bf16(7700 + N, (Hq, 1, D))
+    got, _ = ctx.decode(q, pps=pps)
+    assert_attn_close(got, ctx.oracle(q), f"{pps} pages per split, Hq{Hq} Hkv{Hkv} D{D} N{N}")
+    ctx.close()

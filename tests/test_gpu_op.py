@@ -79,6 +79,14 @@ def test_op_config3_decode_with_append(orc):
     mgr.write_pool(0, 1, vp)
     step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 4, "config3")
     assert mgr.get_layer(0).num_pages == 513
+    # the same op with one split of all pages: each wave walks 129 pages, three
+    # blocks of page ids, and the wave that reads the last page writes the
+    # appended token through the ids it loaded that page with
+    with paged.decode_tuned(600):
+        for i in range(3):
+            step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 5 + i, f"config3, one split, step {i}")
+    assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0)), "K pages"
+    assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1)), "V pages"
     mgr.close()
 
 
@@ -252,6 +260,35 @@ def test_reserve_fits_exact_scheduler_sizing(orc):
         short.reserve_layer(L - 1, max_blocks)
     assert e.value.code == ERR_NO_MEMORY
     short.close()
+
+
+def test_reserve_refuses_workspace_growth_while_staged(orc):
+    """A layer whose decode plans need a larger workspace is refused while
+    another layer is staged for device-position steps (a captured step holds
+    the workspace's address): GENLLM_ERR_INVALID, and nothing of the call is
+    kept -- the pool cursor is where it was, so after sync the same reserve
+    succeeds and the new layer's pools work."""
+    Hq, Hkv, D = 32, 8, 128
+    small, big = 8, 600
+    mgr = paged.PagedAttentionManager(2 * (small + big) * 16 * Hkv * D * 2)
+    mgr.init_layer(0, Hkv, D)
+    mgr.reserve_layer(0, small)
+    mgr.append_kv_pages(0, 20)
+    mgr.stage_decode(0, 8)
+    mgr.init_layer(1, Hkv, D)
+    with pytest.raises(GenllmError) as e:
+        mgr.reserve_layer(1, big)
+    assert e.value.code == ERR_INVALID and "staged" in str(e.value)
+    assert mgr.get_layer(1).max_blocks == 0
+    assert mgr.sync_decode(0) == 20
+    mgr.reserve_layer(1, big)  # fits: the refused call carved nothing
+    assert mgr.get_layer(1).max_blocks == big
+    ref = orc.Manager(with_pool=True)
+    ref.init_layer(1, Hkv, D)
+    ref.reserve_layer(1, big)
+    for i, S in enumerate((40, 1)):
+        step(mgr, ref, 1, Hq, Hkv, S, D, 60 + i, f"after the refused reserve, step {i}")
+    mgr.close()
 
 
 def test_append_kv_from_pos_matches_oracle(orc):

@@ -4,6 +4,10 @@ same kernels and split plan, so the outputs must be bit-identical, on two calls
 in a row -- the second with a smaller input -- and after a call that needs more
 than the fixed scratch, which must be refused without launching anything.
 Also checked against the oracle to the attention tolerance."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -107,3 +111,15 @@ def test_noalloc_refuses_plans_beyond_its_scratch(orc, request):
     q1 = synth.normal_bf16(4248, (32, 1, 128))
     assert np.array_equal(c.run(q1, 8193, noalloc=True), c.run(q1, 8193, noalloc=False))
     c.close()
+
+
+def test_noalloc_first_call_under_capture():
+    """The first call on a device resolves its scratch (hipGetSymbolAddress)
+    and clears the counters with a kernel on the caller's stream; made while
+    a HIP graph is being captured (a fresh process, so it really is the
+    first), the graph's replays equal the workspace entry point bit for bit
+    (tests/noalloc_capture_child.py)."""
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_child.py")
+    r = subprocess.run([sys.executable, child], capture_output=True, text=True, timeout=150)
+    print(r.stdout[-3000:], r.stderr[-3000:])
+    assert r.returncode == 0 and "CAPTURE_OK" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
