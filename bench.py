@@ -115,6 +115,58 @@ def time_kernels(torch, fn, n, warm=5):
     return 1e3 * start.elapsed_time(stop) / n
 
 
+# ----------------------------------------------------------- read floors
+_probe = None
+
+
+def probe_lib():
+    """libgenllm_probe.so (genllm_amd/csrc/probes.hip): read-floor probes that
+    move exactly one kernel's bytes with its access pattern and no arithmetic."""
+    global _probe
+    if _probe is None:
+        import ctypes as C
+        L = C.CDLL(os.path.join(ROOT, "genllm_amd", "libgenllm_probe.so"))
+        P, i32 = C.c_void_p, C.c_int32
+        L.genllm_probe_stream_read.argtypes = [P, C.c_size_t, P, P]
+        L.genllm_probe_decode_read.argtypes = [P, P, P, P, i32, i32, i32, i32, P, P]
+        L.genllm_probe_append_copy.argtypes = [P, P, P, P, P, P, i32, i32, i32, P]
+        _probe = L
+    return _probe
+
+
+def _probe_call(name, *args):
+    rc = getattr(probe_lib(), name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"{name} failed ({rc})")
+
+
+def decode_pps(torch, n_pages, Hkv):
+    """The decode kernel's default split size (about one workgroup per CU)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return max(2, -(-n_pages * Hkv // cus), -(-n_pages // 256))
+
+
+def floor_entry(probe_us, nbytes, kernel_us, what):
+    gbs = nbytes / (probe_us * 1e-6) / 1e9
+    return {"probe_us": round(probe_us, 3), "bytes": nbytes, "GB_s": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "kernel_us": round(kernel_us, 3),
+            "kernel_over_probe": round(kernel_us / probe_us, 3), "probe": what}
+
+
+def stream_floor(torch, nbytes, copies, iters=40):
+    """A contiguous stream of nbytes, rotating over `copies` buffers (more than
+    the 256 MB MALL holds), 16-byte nontemporal loads."""
+    bufs = [torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
+    for b in bufs:
+        b.zero_()
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    us = time_kernels(torch, lambda i: _probe_call("genllm_probe_stream_read", bufs[i % copies].data_ptr(),
+                                                   (nbytes // 16) * 16, sink.data_ptr(), stream), iters)
+    del bufs
+    return us
+
+
 # ----------------------------------------------------------------- headline
 HQ3, HKV3, D3, POOL3, N3 = 32, 8, 128, 2048, 8192
 DECODE_KERNEL_LABEL = ("paged_decode_kernel<128, 8> (split-K attention, split merge in the same launch)"
@@ -219,6 +271,21 @@ def headline(args, np, torch, paged, synth, call):
         sys.exit(3)
     kbytes = decode_kernel_bytes(n_keys)
     achieved = kbytes / (k_mean * 1e-6) / 1e9
+    # read floors: the split kernel's exact page loads without the math (same
+    # plan, same rotating layers), and a contiguous stream of the same bytes
+    n_pages = (n_keys + PAGE - 1) // PAGE
+    pps = decode_pps(torch, n_pages, HKV3)
+    infos = [mgr.get_layer(l) for l in range(L)]
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    cs = torch.cuda.current_stream().cuda_stream
+    pat_us = time_kernels(torch, lambda i: _probe_call(
+        "genllm_probe_decode_read", infos[i % L].k_pool, infos[i % L].v_pool, infos[i % L].k_ids,
+        infos[i % L].v_ids, n_pages, HKV3, D3, pps, sink.data_ptr(), cs), n_k, warm=args.warmup)
+    str_us = stream_floor(torch, kbytes, 16)
+    floors = {"decode_config3_pattern": floor_entry(pat_us, kbytes, k_mean,
+                                                    f"the split kernel's page loads, {pps} pages per split, no math, "
+                                                    "no merge"),
+              "decode_config3_stream": floor_entry(str_us, kbytes, k_mean, "contiguous stream of the same bytes")}
     res = {
         "value": round(total_bytes / (step_s * args.steps) / 1e9, 1),
         "ms_per_step": round(step_s * 1e3, 5),
@@ -239,6 +306,7 @@ def headline(args, np, torch, paged, synth, call):
                      "bytes_per_launch": kbytes, "avg_launch_us": round(k_mean, 3), "launches": n_k,
                      "timing": "one HIP event pair on the launch stream around back-to-back launches (GPU kept "
                                "fed: host queued ahead behind a spin kernel) / launches"},
+        "read_floor": floors,
     }
     return res, mgr, seed
 
@@ -276,12 +344,26 @@ def append_cfg2(np, torch, paged, synth, call):
     # the first chunk of every copy is the timing warm-up, the other three are timed
     avg_us = time_kernels(torch, app, n_app - copies, warm=copies)
     app_bytes = 2 * S * Hkv * D * 2 * 2 + S * (D // 2) * 4 * 2 + D * 4 + (S // PAGE) * 8
+    # read floor: the same K/V rows moved into 256 shuffled pages of each copy's
+    # pool with the kernel's lane map, no norm or RoPE
+    ids = [(torch.from_numpy(synth.shuffled(seed + 2 * c, pool)[:S // PAGE].astype("int32")).cuda(),
+            torch.from_numpy(synth.shuffled(seed + 2 * c + 1, pool)[:S // PAGE].astype("int32")).cuda())
+           for c in range(copies)]
+    infos = [m2.get_layer(c) for c in range(copies)]
+    cs = torch.cuda.current_stream().cuda_stream
+    cp_us = time_kernels(torch, lambda i: _probe_call(
+        "genllm_probe_append_copy", ks[i % copies].data_ptr(), vs[i % copies].data_ptr(), infos[i % copies].k_pool,
+        infos[i % copies].v_pool, ids[i % copies][0].data_ptr(), ids[i % copies][1].data_ptr(), S, Hkv, D, cs),
+        n_app - copies, warm=copies)
+    copy_bytes = 2 * S * Hkv * D * 2 * 2
     m2.close()
     gbs = app_bytes / (avg_us * 1e-6) / 1e9
     return {"avg_launch_us": round(avg_us, 3), "bytes": app_bytes, "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "launches": n_app - copies,
             "note": "GPU time of the C call (qk_norm_rope_append: host page allocation, then kv_append_kernel with "
-                    "the 256 new page ids in its launch arguments), back to back, GPU kept fed"}
+                    "the 256 new page ids in its launch arguments), back to back, GPU kept fed",
+            "read_floor": floor_entry(cp_us, copy_bytes, avg_us, "the kernel's K/V row movement into shuffled pages "
+                                      "(its lane map and stores), no norm, RoPE or tables")}
 
 
 def prefill_cfg4(np, torch, paged, synth, call, iters=40):
@@ -506,6 +588,26 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
                                1.0 / np.sqrt(D), ws)
 
     avg_us = time_kernels(torch, all_layers, iters, warm=2)
+    # read floors: the split kernel's page loads of all 36 layers without the
+    # math, and a contiguous stream of one layer's bytes
+    pps = decode_pps(torch, n_pages, Hkv)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    cs = torch.cuda.current_stream().cuda_stream
+
+    def all_probes(_):
+        for l in range(layers):
+            inf = infos[l]
+            _probe_call("genllm_probe_decode_read", inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, n_pages, Hkv, D, pps,
+                        sink.data_ptr(), cs)
+
+    pat_us = time_kernels(torch, all_probes, iters, warm=2) / layers
+    layer_bytes = decode_kernel_bytes(N)
+    str_us = stream_floor(torch, layer_bytes, 8, iters=20)
+    floors = {"decode_config5_pattern": floor_entry(pat_us, layer_bytes, avg_us / layers,
+                                                    f"the split kernel's page loads per layer, {pps} pages per split, "
+                                                    "no math, no merge"),
+              "decode_config5_stream": floor_entry(str_us, layer_bytes, avg_us / layers,
+                                                   "contiguous stream of one layer's bytes")}
     # the same 36-layer sequence captured once into a HIP graph and replayed
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -541,6 +643,7 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
             "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "graph_total_us": round(g_us, 2), "graph_us_per_layer": round(g_us / layers, 3),
             "graph_GB_s": round(b5 / (g_us * 1e-6) / 1e9, 1),
+            "read_floor": floors,
             "decode_loop_graph": {"us_per_token": round(s_us, 2), "us_per_layer": round(s_us / layers, 3),
                                   "GB_s": round(s_bytes / (s_us * 1e-6) / 1e9, 1), "tokens": iters,
                                   "note": "36-layer append + attend step captured once at the device position "
@@ -808,6 +911,8 @@ def main():
         "step_timing": head["step_timing"],
         "host": head["host"],
     }
+    if args.only:
+        result["read_floor"] = head["read_floor"]
     result["host"]["cpp_us_per_call"] = cpp_host["host_us_per_call"] if cpp_host else None
     result["host"]["cpp_note"] = ("host time of one PAGED_ATTN dispatch through kernel::dispatch, from C++ "
                                   "(tests/cpp/test_ops_hip --host-cost): " + cpp_host_note)
@@ -822,6 +927,12 @@ def main():
         result["secondary"] = {"append_config2": append_cfg2(*common), "prefill_config4": prefill_cfg4(*common),
                                "flash_config4": flash_cfg4(*common), "qwen35_head_dim_256": qwen35_d256(*common),
                                "longctx_config5": longctx_cfg5(*common), "linear_qkv_4b": linear_qkv(*common)}
+        # read floors (probes that move each kernel's bytes with its access
+        # pattern and no arithmetic), next to the kernels they bound
+        sec = result["secondary"]
+        result["secondary"]["read_floor"] = {
+            **head["read_floor"], **sec["longctx_config5"].pop("read_floor"),
+            "append_config2_copy": sec["append_config2"].pop("read_floor")}
     if not args.skip_cpu and not args.only:
         result["cpu_baseline"] = cpu_baseline(mgr, np, paged, synth, args, seed)
     mgr.close()
