@@ -30,6 +30,7 @@ _NAMES = {1: "INVALID", 2: "UNSUPPORTED", 3: "NO_MEMORY", 4: "POOL_FULL", 5: "HI
 
 PAGE = 16
 DTYPE_BF16 = 30
+DTYPE_F16 = 1
 
 
 class GenllmError(RuntimeError):

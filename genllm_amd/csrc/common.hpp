@@ -114,6 +114,59 @@ __device__ __forceinline__ f32x4_t mfma16x16x16(const s16x4_t& a, const s16x4_t&
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
+// ------------------------------------------------------------ element type
+// fp32 -> fp16 as float16_t's constructor (float16.hpp, float_to_f16_bits):
+// round to nearest even with gradual underflow, overflow to infinity -- the
+// hardware conversion -- except that a NaN becomes an infinity of its sign.
+__device__ __forceinline__ uint32_t f32_to_f16_ref(float f) {
+    const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    return f != f ? ((__float_as_uint(f) >> 16) & 0x8000u) | 0x7C00u : h;
+}
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t_ __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t_ __attribute__((ext_vector_type(2)));
+
+// The 16-bit element type of q, the K/V pools and out: bf16 (F16 = false,
+// every Qwen3 layer) or fp16.  The MFMAs take raw 16-byte (8 elements) or
+// 8-byte (4 elements) operands: both types have the same lane layouts.
+template <bool F16>
+struct Elem;
+template <>
+struct Elem<false> {
+    static __device__ __forceinline__ f32x4_t mma32(const uint4& a, const uint4& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4_t mma16(const uint2& a, const uint2& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
+                                                        c, 0, 0, 0);
+    }
+    // two probabilities, round to nearest even (one v_cvt_pk_bf16_f32)
+    static __device__ __forceinline__ uint32_t pack_p(float lo, float hi) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t_{lo, hi}, bf16x2_t_));
+    }
+    // an output element as the reference's from_f32_rt stores it
+    static __device__ __forceinline__ uint32_t out(float f) { return f32_to_bf16_ref(f); }
+};
+template <>
+struct Elem<true> {
+    static __device__ __forceinline__ f32x4_t mma32(const uint4& a, const uint4& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                      0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4_t mma16(const uint2& a, const uint2& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                     0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack_p(float lo, float hi) {
+        return __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(lo), static_cast<_Float16>(hi)});
+    }
+    static __device__ __forceinline__ uint32_t out(float f) { return f32_to_f16_ref(f); }
+};
+
 // Host helpers
 int device_cu_count();
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

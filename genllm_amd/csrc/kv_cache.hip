@@ -603,9 +603,11 @@ int op_params(const LayerState& s, const void* q, const void* k, const void* v, 
               float scale, int32_t causal, int32_t n_after, AttnParams& p) {
     if (head_dim != 128 && head_dim != 256)
         return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention requires head_dim 128 or 256");
-    if (batch != 1) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention: batch must be 1");
-    if (s.dtype != GENLLM_DTYPE_BF16 || s.head_dim != head_dim || s.n_kv_heads != n_kv_heads)
-        return fail(GENLLM_ERR_INVALID, "paged_attention: tensor shape/dtype differs from the layer's pools");
+    if (batch < 1) return fail(GENLLM_ERR_INVALID, "paged_attention: batch must be >= 1");
+    if (s.dtype != GENLLM_DTYPE_BF16 && s.dtype != GENLLM_DTYPE_F16)
+        return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention: layer dtype must be bf16 or f16");
+    if (s.head_dim != head_dim || s.n_kv_heads != n_kv_heads)
+        return fail(GENLLM_ERR_INVALID, "paged_attention: tensor shape differs from the layer's pools");
     if (n_kv_groups <= 0 || n_q_heads != n_kv_heads * n_kv_groups)
         return fail(GENLLM_ERR_INVALID, "paged_attention: n_q_heads must equal n_kv_heads * n_kv_groups");
     if (!q || !k || !v || !out) return fail(GENLLM_ERR_INVALID, "paged_attention: null tensor");
@@ -631,6 +633,7 @@ int op_params(const LayerState& s, const void* q, const void* k, const void* v, 
     p.G = n_kv_groups;
     p.scale_log2 = scale * kLog2e;
     p.causal = causal != 0;
+    p.f16 = s.dtype == GENLLM_DTYPE_F16;
     p.page_elems = int64_t(kPage) * n_kv_heads * head_dim;
     p.kv_row = int64_t(n_kv_heads) * head_dim;
     return GENLLM_OK;
@@ -725,6 +728,23 @@ extern "C" int genllm_paged_attention(genllm_kv* kv, int32_t layer, const void* 
     if (int rc = launch_attention(p, head_dim, st)) {
         if (fuse) undo_append(*s, undo);  // nothing ran: the fused append is part of this launch
         return rc;
+    }
+    // 3. batch entries after the first attend over the same cache
+    // (attention.cpp:156: the loop over b reads one page table; the append
+    // above took the first entry's K/V rows, as append_kv_from_tensor reads
+    // K->data for n_kv_heads x seq_len rows): attention only, after the first
+    // entry's launch has written the new rows and page ids.
+    if (batch > 1) {
+        AttnParams pb = p;
+        pb.k_new = pb.v_new = nullptr;
+        pb.new_from = INT32_MAX;
+        pb.upd.count = 0;
+        const int64_t entry = int64_t(n_q_heads) * seq_len * head_dim;
+        for (int32_t b = 1; b < batch; ++b) {
+            pb.q = p.q + b * entry;
+            pb.out = p.out + b * entry;
+            if (int rc = launch_attention(pb, head_dim, st)) return rc;
+        }
     }
     return GENLLM_OK;
 }
@@ -826,6 +846,7 @@ extern "C" int genllm_paged_attention_step(genllm_kv* kv, int32_t layer, const v
     if (!s->staged) return fail(GENLLM_ERR_INVALID, "paged_attention_step: layer not staged (genllm_kv_stage_decode)");
     if (seq_len <= 0 || int64_t(n_kv_groups) * seq_len > 16)
         return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention_step: seq_len * n_kv_groups must be in [1, 16]");
+    if (batch != 1) return fail(GENLLM_ERR_UNSUPPORTED, "paged_attention_step: batch must be 1");
     // Planned for the end of the staged window: the grid covers every page a
     // step inside it can reach; splits past a step's last page are empty.
     const int32_t window_end = std::max(s->num_cached, seq_len);

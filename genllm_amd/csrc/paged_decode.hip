@@ -75,11 +75,6 @@ constexpr int kNonTemporal = 2;    // buffer-access cache policy bit nt (gfx950:
 constexpr int kCoherent = 16;
 typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
-    const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
-    return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
-}
-
 // Buffer resource over the split partials: o [Hkv][split][row][D], then
 // {m, l} [Hkv][split][row].
 template <int D>
@@ -100,7 +95,7 @@ __device__ __forceinline__ auto part_rsrc(const AttnParams& p) {
 // invalidate is needed.  Merge work: W waves over (row, split) pairs -- for
 // R < W rows, W/R waves share a row's splits -- with up to kMergeU splits in
 // flight per lane, then the per-wave states meet in LDS.
-template <int D, int W>
+template <int D, int W, bool F16>
 __device__ __forceinline__ void merge_last_arrival(const AttnParams& p, int h, float (&lds_m)[W][kRows],
                                                    float (&lds_l)[W][kRows], float (&lds_o)[W][kRows][D + 4]) {
     constexpr int VH = D / 128;
@@ -197,7 +192,21 @@ __device__ __forceinline__ void merge_last_arrival(const AttnParams& p, int h, f
 #pragma unroll
         for (int hh = 0; hh < VH; ++hh)
             *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
-                pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
+                pack2(Elem<F16>::out(O0[hh] * inv), Elem<F16>::out(O1[hh] * inv));
+    }
+}
+
+// Two probabilities as the PV MFMA's 16-bit operand, round to nearest even.
+// bf16: converted one by one and packed (measured 0.15 us faster per config-3
+// decode than one v_cvt_pk_bf16_f32 per pair, which the compiler schedules
+// differently around the V^T reads).
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_p(float lo, float hi) {
+    if constexpr (F16) {
+        return Elem<true>::pack_p(lo, hi);
+    } else {
+        const __bf16 a = static_cast<__bf16>(lo), b = static_cast<__bf16>(hi);
+        return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
     }
 }
 
@@ -215,8 +224,9 @@ __device__ __forceinline__ int step_load(const int32_t* at) {
         __hip_atomic_load(const_cast<int32_t*>(at), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-template <int D, int W, bool kStep>
+template <int D, int W, bool kStep, bool F16>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
+    using E = Elem<F16>;
     static_assert(D == 128 || D == 256, "decode kernel: head_dim 128 or 256");
     constexpr int KS = D / 32;   // S^T k-steps
     constexpr int DB = D / 16;   // O^T dim blocks
@@ -241,14 +251,14 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     // the step's own end.)
     const int r = n16;  // this lane's row (MFMA column): q head h*G + r%G, query r/G
     const bool row_ok = r < rows_total;
-    bf16x8_t qb[KS];
+    uint4 qb[KS];  // Q^T operand chunks (raw 16-bit elements)
     {
         const uint16_t* qrow = p.q + int64_t(h * p.G + r % p.G) * p.q_head_stride + int64_t(r / p.G) * p.q_tok_stride;
 #pragma unroll
         for (int c = 0; c < KS; ++c) {
             uint4 u = make_uint4(0, 0, 0, 0);
             if (row_ok) u = *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g);
-            qb[c] = as_bf16x8(u);
+            qb[c] = u;
         }
     }
     const int begin = sp * p.pages_per_split;
@@ -419,7 +429,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         // S^T = K Q^T
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < KS; ++c) s = mfma16x16x32(as_bf16x8(pr.k[c]), qb[c], s);
+        for (int c = 0; c < KS; ++c) s = E::mma32(pr.k[c], qb[c], s);
         // Rows past rows_total have q = 0 (score 0) and are never written out.
         float x[4], lmx = -INFINITY;
 #pragma unroll
@@ -451,15 +461,13 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
             sum += pw[i];
         }
         l_run += sum;
-        const s16x4_t pb =
-            __builtin_bit_cast(s16x4_t, make_uint2(bf16x2_rne(pw[0], pw[1]), bf16x2_rne(pw[2], pw[3])));
+        const uint2 pb = make_uint2(pack_p<F16>(pw[0], pw[1]), pack_p<F16>(pw[2], pw[3]));
         __builtin_amdgcn_wave_barrier();
         // O^T += V^T P^T
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-            const s16x4_t a =
-                __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(&vt[(16 * db + n16) * VT_ROW + 4 * g]));
-            acc[db] = mfma16x16x16(a, pb, acc[db]);
+            const uint2 a = *reinterpret_cast<const uint2*>(&vt[(16 * db + n16) * VT_ROW + 4 * g]);
+            acc[db] = E::mma16(a, pb, acc[db]);
         }
         __builtin_amdgcn_wave_barrier();
     };
@@ -568,7 +576,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 #pragma unroll
             for (int hh = 0; hh < VH; ++hh)
                 *reinterpret_cast<uint32_t*>(orow + 128 * hh + 2 * lane) =
-                    pack2(f32_to_bf16_ref(O0[hh] * inv), f32_to_bf16_ref(O1[hh] * inv));
+                    pack2(E::out(O0[hh] * inv), E::out(O1[hh] * inv));
         } else {
             // partials: o [h][split][row][D], then {m, l} [h][split][row],
             // stored agent-coherent (sc1: the store completes at the device's
@@ -605,7 +613,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
             }
         }
     }
-    if (p.counters && p.n_splits > 1) merge_last_arrival<D, W>(p, h, lds_m, lds_l, lds_o);
+    if (p.counters && p.n_splits > 1) merge_last_arrival<D, W, F16>(p, h, lds_m, lds_l, lds_o);
 }
 
 // Merge of the splits: one workgroup of MW waves per (kv head, row, 64-dim
@@ -622,7 +630,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 // box, 128-dim blocks against 64: Qwen3.5 (D = 256, 103 splits) 12.8 -> 12.3
 // us per decode, config 3 13.1 -> 12.9 us (whole rows measured 14.2 us on the
 // Qwen3.5 shape, on a box where config 3 took 13.6).
-template <int D, int MW>
+template <int D, int MW, bool F16>
 __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams p) {
     constexpr int U = kMergeU;  // splits in flight per lane
     constexpr int PL = 1;       // dims per lane (the workgroup's kMergeDims dims)
@@ -707,7 +715,7 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
         const float inv = 1.0f / L;
         uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride +
                          d0 + PL * lane;
-        *orow = uint16_t(f32_to_bf16_ref(O[0] * inv));
+        *orow = uint16_t(Elem<F16>::out(O[0] * inv));
     }
 }
 
@@ -790,33 +798,33 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
     return GENLLM_OK;
 }
 
-template <int D, bool kStep>
+template <int D, bool kStep, bool F16>
 void launch_split(const AttnParams& p, hipStream_t stream) {
     bool wide = false;
     if constexpr (D == 128) {
         wide = p.pages_per_split <= kWideMaxPps;
         if (wide)
-            hipLaunchKernelGGL((paged_decode_kernel<D, kWideWaves, kStep>), dim3(p.Hkv, p.n_splits),
+            hipLaunchKernelGGL((paged_decode_kernel<D, kWideWaves, kStep, F16>), dim3(p.Hkv, p.n_splits),
                                dim3(kWideWaves * 64), 0, stream, p);
     }
     if (!wide)
-        hipLaunchKernelGGL((paged_decode_kernel<D, kWaves, kStep>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64), 0,
-                           stream, p);
+        hipLaunchKernelGGL((paged_decode_kernel<D, kWaves, kStep, F16>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64),
+                           0, stream, p);
 }
 
-template <int D>
+template <int D, bool F16>
 int launch_decode_d(const AttnParams& p, hipStream_t stream) {
     if (p.step)
-        launch_split<D, true>(p, stream);
+        launch_split<D, true, F16>(p, stream);
     else
-        launch_split<D, false>(p, stream);
+        launch_split<D, false, F16>(p, stream);
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1 && !p.counters) {
         const dim3 grid(p.Hkv, p.G * p.S, D / kMergeDims);
         if (p.n_splits > 4 * kMergeU)
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8>), grid, dim3(8 * 64), 0, stream, p);
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8, F16>), grid, dim3(8 * 64), 0, stream, p);
         else
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4>), grid, dim3(4 * 64), 0, stream, p);
+            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4, F16>), grid, dim3(4 * 64), 0, stream, p);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;
@@ -827,7 +835,8 @@ int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (p.n_pages <= 0) return GENLLM_OK;
     if (p.n_splits > kMaxSplits || p.pages_per_split <= 0 || p.G * p.S > kRows)
         return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
-    return head_dim == 128 ? launch_decode_d<128>(p, stream) : launch_decode_d<256>(p, stream);
+    if (p.f16) return head_dim == 128 ? launch_decode_d<128, true>(p, stream) : launch_decode_d<256, true>(p, stream);
+    return head_dim == 128 ? launch_decode_d<128, false>(p, stream) : launch_decode_d<256, false>(p, stream);
 }
 
 }  // namespace genllm

@@ -107,8 +107,9 @@ __device__ __forceinline__ void tile_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
-template <int D>
+template <int D, bool F16>
 __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
+    using E = Elem<F16>;
     constexpr int KS = D / 32, DB = D / 16;
     constexpr int ROWB = D * 2;       // bytes per token row (256 or 512)
     constexpr int TILEB = KT * ROWB;  // bytes of K (or V) per tile
@@ -142,12 +143,12 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
 
     // Q^T operands: lane -> query q0 + n16, dims 32ks + 8g..+7 (a query past
     // the chunk loads the last row: its column stays finite and is not written)
-    bf16x8_t qb[KS];
+    uint4 qb[KS];  // raw 16-bit elements
     {
         const int s = min(q0 + n16, p.S - 1);
         const uint16_t* qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(s) * p.q_tok_stride;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qb[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g));
+        for (int ks = 0; ks < KS; ++ks) qb[ks] = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
     }
     float m = -INFINITY, l = 0.0f;
     // nm = -m (0 while m = -inf); th = the raw score above which the scaled
@@ -239,7 +240,7 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
                 const int pos = 16 * (ks >> 2) + ((4 * (ks & 3) + g) ^ swz(n16));
                 const u32x4_t a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
                     buf + (row * ROWB + pos * 16));
-                s[kb] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a), qb[ks], s[kb]);
+                s[kb] = E::mma32(__builtin_bit_cast(uint4, a), qb[ks], s[kb]);
             }
         after_s();
         if (masked) {
@@ -276,9 +277,8 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) e[kb][i] = exp2_fast(__builtin_fmaf(s[kb][i], c, nm));
         l += ((e[0][0] + e[0][1]) + (e[0][2] + e[0][3])) + ((e[1][0] + e[1][1]) + (e[1][2] + e[1][3]));
-        const bf16x8_t pb = __builtin_bit_cast(
-            bf16x8_t, u32x4_t{bf16_pair_rne(e[0][0], e[0][1]), bf16_pair_rne(e[0][2], e[0][3]),
-                              bf16_pair_rne(e[1][0], e[1][1]), bf16_pair_rne(e[1][2], e[1][3])});
+        const uint4 pb = make_uint4(E::pack_p(e[0][0], e[0][1]), E::pack_p(e[0][2], e[0][3]),
+                                    E::pack_p(e[1][0], e[1][1]), E::pack_p(e[1][2], e[1][3]));
         // V^T from two transposing reads per 16 dims: rows r0 + 4g + n16/4 and
         // + 16, dims 16db + 4(n16%4)..+3 (chunk 2db + (n16%4)/2, half n16%2);
         // each read's LDS offset is one integer added to the buffer base, which
@@ -294,7 +294,7 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
             const s16x4_t lo = ds_read_tr(buf + off0);
             const s16x4_t hi = ds_read_tr(buf + off1);
             const s16x4_t a8[2] = {lo, hi};
-            acc[db] = mfma16x16x32(__builtin_bit_cast(bf16x8_t, a8), pb, acc[db]);
+            acc[db] = E::mma32(__builtin_bit_cast(uint4, a8), pb, acc[db]);
         }
     };
 
@@ -378,8 +378,13 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (acc[db][i] * a0 + xch[(db * 4 + i) * 64] * a1) * inv;
         uint2 w;
-        w.x = bf16_pair_out(o[0], o[1]);
-        w.y = bf16_pair_out(o[2], o[3]);
+        if constexpr (F16) {
+            w.x = pack2(E::out(o[0]), E::out(o[1]));
+            w.y = pack2(E::out(o[2]), E::out(o[3]));
+        } else {
+            w.x = bf16_pair_out(o[0], o[1]);
+            w.y = bf16_pair_out(o[2], o[3]);
+        }
         *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = w;
     }
 }
@@ -388,8 +393,10 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
 // (4 waves per SIMD: at config 4 36.2 us, against 41.9 us for the earlier
 // form of one 128 KB, 196-VGPR workgroup per CU running two query tiles of
 // 2 x 32 queries, A/B on one box); D = 256: 128 KB, one workgroup per CU.
-__global__ __launch_bounds__(WAVES * 64, 2) void paged_prefill_d128_kernel(AttnParams p) { prefill_tiles<128>(p); }
-__global__ __launch_bounds__(WAVES * 64) void paged_prefill_d256_kernel(AttnParams p) { prefill_tiles<256>(p); }
+template <bool F16>
+__global__ __launch_bounds__(WAVES * 64, 2) void paged_prefill_d128_kernel(AttnParams p) { prefill_tiles<128, F16>(p); }
+template <bool F16>
+__global__ __launch_bounds__(WAVES * 64) void paged_prefill_d256_kernel(AttnParams p) { prefill_tiles<256, F16>(p); }
 
 }  // namespace
 
@@ -398,9 +405,11 @@ int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream) 
     if (p.S <= 0 || p.n_pages <= 0) return GENLLM_OK;
     const dim3 grid(unsigned(int64_t((p.S + QT - 1) / QT) * p.Hq)), block(WAVES * 64);
     if (head_dim == 128)
-        hipLaunchKernelGGL(paged_prefill_d128_kernel, grid, block, 0, stream, p);
+        hipLaunchKernelGGL(p.f16 ? paged_prefill_d128_kernel<true> : paged_prefill_d128_kernel<false>, grid, block, 0,
+                           stream, p);
     else
-        hipLaunchKernelGGL(paged_prefill_d256_kernel, grid, block, 0, stream, p);
+        hipLaunchKernelGGL(p.f16 ? paged_prefill_d256_kernel<true> : paged_prefill_d256_kernel<false>, grid, block, 0,
+                           stream, p);
     GENLLM_LAUNCH_CHECK("paged_prefill kernel");
     return GENLLM_OK;
 }

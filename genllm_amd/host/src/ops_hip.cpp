@@ -41,7 +41,15 @@ void PagedAttentionImpl<Device::HIP>::execute(Tensor* out, int32_t dev_id) {
     const Tensor* Q = out->src[0];
     const Tensor* K = out->src[1];
     const Tensor* V = out->src[2];
-    for (const Tensor* t : {Q, K, V, static_cast<const Tensor*>(out)}) require_bf16(t, "paged_attention");
+    // q, k, v and out are of the layer's element type, bf16 or fp16 (the
+    // reference reads K/V as Q's dtype, attention.cpp:186-200)
+    genllm_layer_info info{};
+    genllm_check(genllm_kv_layer_info(mgr->handle(), layer_id, &info), "paged_attention");
+    const DataType dt = static_cast<DataType>(info.dtype);
+    if (dt != DataType::GGML_TYPE_BF16 && dt != DataType::GGML_TYPE_F16)
+        throw std::runtime_error("paged_attention: HIP kernels take bf16 or f16 layers");
+    for (const Tensor* t : {Q, K, V, static_cast<const Tensor*>(out)})
+        if (!t || t->dtype != dt) throw std::runtime_error("paged_attention: tensor dtype differs from the layer's");
 
     const int32_t batch = int32_t(Q->dims[0]);
     const int32_t num_q_heads = int32_t(Q->dims[1]);

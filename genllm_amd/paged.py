@@ -18,7 +18,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import DTYPE_BF16, PAGE, GenllmError, LayerInfo, call, lib
+from ._lib import DTYPE_BF16, DTYPE_F16, PAGE, GenllmError, LayerInfo, call, lib
 
 
 def _stream(stream) -> int | None:
@@ -223,11 +223,13 @@ class PagedAttentionManager:
 # ------------------------------------------------------------------ the op
 def paged_attention(mgr: PagedAttentionManager, layer: int, q, k, v, out, n_kv_groups: int, scale: float,
                     causal: bool = True, stream=None):
-    """PagedAttentionImpl<HIP>::execute: q/out [1,Hq,S,D], k/v [1,Hkv,S,D] bf16 (head-major)."""
+    """PagedAttentionImpl<HIP>::execute: q/out [B,Hq,S,D], k/v [B,Hkv,S,D] head-major, of the
+    layer's element type (bf16 or float16); every batch entry attends the one cache and the
+    first entry's k/v rows are appended, as in the reference."""
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     for t in (q, k, v, out):
-        assert t.dtype == torch.bfloat16 and t.is_contiguous()
+        assert t.dtype in (torch.bfloat16, torch.float16) and t.dtype == q.dtype and t.is_contiguous()
     call("genllm_paged_attention", mgr.handle, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, Hq, S, D, Hkv,
          n_kv_groups, float(scale), int(causal), _stream(stream))
 
@@ -238,7 +240,7 @@ def paged_attention_step(mgr: PagedAttentionManager, layer: int, q, k, v, out, n
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     for t in (q, k, v, out):
-        assert t.dtype == torch.bfloat16 and t.is_contiguous()
+        assert t.dtype in (torch.bfloat16, torch.float16) and t.dtype == q.dtype and t.is_contiguous()
     call("genllm_paged_attention_step", mgr.handle, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, Hq, S, D, Hkv,
          n_kv_groups, float(scale), int(causal), _stream(stream))
 
@@ -410,6 +412,11 @@ def to_device_bf16(bits: np.ndarray) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).cuda()
 
 
+def to_device_f16(bits: np.ndarray) -> torch.Tensor:
+    """fp16 bit patterns (uint16 numpy) -> GPU float16 tensor."""
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).view(torch.float16).cuda()
+
+
 def to_host_bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
@@ -417,5 +424,6 @@ def to_host_bits(t: torch.Tensor) -> np.ndarray:
 __all__ = [
     "PagedAttentionManager", "paged_attention", "qk_norm_rope_append", "rms_norm", "apply_rope", "rope_cache",
     "kv_scatter", "paged_decode", "paged_decode_noalloc", "paged_prefill", "flash_attention", "decode_workspace_bytes", "fill_normal_bf16",
-    "selftest_mfma", "device_view", "to_device_bf16", "to_host_bits", "GenllmError", "PAGE", "DTYPE_BF16",
+    "selftest_mfma", "device_view", "to_device_bf16", "to_device_f16", "to_host_bits", "GenllmError", "PAGE",
+    "DTYPE_BF16", "DTYPE_F16",
 ]

@@ -67,6 +67,13 @@ def normal_bf16(seed: int, shape, offset: int = 0) -> np.ndarray:
     return f32_to_bf16_bits(normal_f32(seed, n, offset)).reshape(shape)
 
 
+def normal_f16(seed: int, shape, offset: int = 0) -> np.ndarray:
+    """Bit patterns of N(0,1) samples rounded to nearest-even fp16 (inputs of
+    the fp16 KV-pool tests)."""
+    n = int(np.prod(shape))
+    return normal_f32(seed, n, offset).astype(np.float16).view(np.uint16).reshape(shape)
+
+
 def uniform_f32(seed: int, shape, lo: float, hi: float, offset: int = 0) -> np.ndarray:
     n = int(np.prod(shape))
     h = _hash(seed, n, offset)

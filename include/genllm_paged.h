@@ -37,6 +37,7 @@ extern "C" {
 
 #define GENLLM_PAGE_BLOCK_SIZE 16 /* include/core/page_attention.h:9 */
 #define GENLLM_DTYPE_BF16 30      /* DataType::GGML_TYPE_BF16, include/utils/utils.hpp:59 */
+#define GENLLM_DTYPE_F16 1        /* DataType::GGML_TYPE_F16 */
 
 /* Message for the last failing call on this thread ("" if none). */
 const char *genllm_last_error(void);
@@ -123,8 +124,13 @@ int genllm_kv_block_free(genllm_kv *kv, int32_t layer, int32_t which, int32_t id
 /* ---------------------------------------------------------------- the op
  * PagedAttentionImpl<D>::execute (src/backend/cpu/attention.cpp:123-216,
  * src/backend/cuda/attention.cu:491-580): append this step's K/V to the layer's
- * pages, then attend.  q, out: head-major [batch=1][n_q_heads][seq_len][head_dim];
- * k, v: [1][n_kv_heads][seq_len][head_dim] (op_factory.hpp:413-476).  scale,
+ * pages, then attend.  q, out: head-major [batch][n_q_heads][seq_len][head_dim];
+ * k, v: [batch][n_kv_heads][seq_len][head_dim] (op_factory.hpp:413-476), of
+ * the layer's element type (genllm_kv_init_layer: GENLLM_DTYPE_BF16 or
+ * GENLLM_DTYPE_F16; the reference reads K/V as Q's dtype, attention.cpp:
+ * 186-200).  As in the reference, every batch entry attends over the layer's
+ * one cache and only the first entry's k/v rows are appended (attention.cpp:
+ * 146, 156; append_kv_from_tensor reads n_kv_heads x seq_len rows).  scale,
  * causal and n_kv_groups are op_params[1..3].  An inactive layer returns
  * GENLLM_OK without touching out (attention.cpp:127).  head_dim 128 (Qwen3)
  * and 256 (Qwen3.5, Qwen35.hpp:14-16) are served; any other returns

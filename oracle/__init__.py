@@ -20,6 +20,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _SO = os.path.join(_HERE, "liboracle.so")
 
 BF16 = 30
+F16 = 1
 PAGE = 16
 
 
@@ -51,6 +52,11 @@ _sz = C.c_size_t
 
 def _declare(L):
     sig = {
+        "or_f32_to_f16": (C.c_uint16, [_f]),
+        "or_f16_to_f32": (_f, [C.c_uint16]),
+        "or_paged_attention_dt": (C.c_int, [_P, _i32, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f,
+                                            C.c_int, _i32]),
+        "or_paged_attend_dt": (C.c_int, [_P, _i32, _P, _P, _i32, _i32, _i32, _i32, _i32, _i32, _f, C.c_int, _i32]),
         "or_f32_to_bf16": (C.c_uint16, [_f]),
         "or_bf16_to_f32": (_f, [C.c_uint16]),
         "or_f32_to_bf16_array": (None, [_P, _P, _sz]),
@@ -117,6 +123,20 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
 def bf16_to_f32(b: np.ndarray) -> np.ndarray:
     b = np.ascontiguousarray(b, dtype=np.uint16)
     return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    """float16_t(float) bit patterns (or_f32_to_f16, one call per element)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    f = lib().or_f32_to_f16
+    return np.array([f(float(v)) for v in x.ravel()], dtype=np.uint16).reshape(x.shape)
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    """float(float16_t) (or_f16_to_f32, one call per element)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    f = lib().or_f16_to_f32
+    return np.array([f(int(v)) for v in h.ravel()], dtype=np.float32).reshape(h.shape)
 
 
 def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
@@ -308,23 +328,24 @@ class Manager:
         buf = (C.c_uint16 * n).from_address(base)
         return np.ctypeslib.as_array(buf).reshape(mb, PAGE, Hkv, D)
 
-    def paged_attention(self, layer, Q, K, V, groups, scale, causal=True):
-        """PagedAttentionImpl<CPU>::execute; Q [1,Hq,S,D], K/V [1,Hkv,S,D]."""
+    def paged_attention(self, layer, Q, K, V, groups, scale, causal=True, dtype=BF16):
+        """PagedAttentionImpl<CPU>::execute; Q [B,Hq,S,D], K/V [B,Hkv,S,D] bit patterns of
+        `dtype` (BF16 or F16)."""
         Q = np.ascontiguousarray(Q, dtype=np.uint16)
         K = np.ascontiguousarray(K, dtype=np.uint16)
         V = np.ascontiguousarray(V, dtype=np.uint16)
         B, Hq, S, D = Q.shape
         out = np.zeros_like(Q)
-        rc = lib().or_paged_attention(self._h, layer, ptr(Q), ptr(K), ptr(V), ptr(out), B, Hq, S, D,
-                                      K.shape[1], groups, scale, int(causal))
+        rc = lib().or_paged_attention_dt(self._h, layer, ptr(Q), ptr(K), ptr(V), ptr(out), B, Hq, S, D,
+                                         K.shape[1], groups, scale, int(causal), dtype)
         return out, rc
 
-    def paged_attend(self, layer, Q, n_kv_heads, groups, scale, causal=True):
+    def paged_attend(self, layer, Q, n_kv_heads, groups, scale, causal=True, dtype=BF16):
         Q = np.ascontiguousarray(Q, dtype=np.uint16)
         B, Hq, S, D = Q.shape
         out = np.zeros_like(Q)
-        rc = lib().or_paged_attend(self._h, layer, ptr(Q), ptr(out), B, Hq, S, D, n_kv_heads, groups, scale,
-                                   int(causal))
+        rc = lib().or_paged_attend_dt(self._h, layer, ptr(Q), ptr(out), B, Hq, S, D, n_kv_heads, groups, scale,
+                                      int(causal), dtype)
         return out, rc
 
     def qk_norm_rope_append(self, layer, k_tok, v_tok, gamma_k, eps, cos, sin, start_pos,

@@ -1,7 +1,8 @@
 /* attention.c -- TEST INFRASTRUCTURE ONLY (see oracle.h).
  *
  * PagedAttentionImpl<CPU>::execute (src/backend/cpu/attention.cpp:123-216) and
- * FlashAttentionImpl<CPU>::execute (:39-121) for bf16 tensors, single thread,
+ * FlashAttentionImpl<CPU>::execute (:39-121) for bf16 (and, for the paged op,
+ * fp16) tensors, single thread,
  * per-token online softmax in fp32 exactly as written there:
  *   score = (sum_d q[d]*k[d]) * scale               (:184-192, fma chain)
  *   m' = fmax(m, score); e_s = exp(score-m'); e_p = exp(m-m')   (:194-197)
@@ -18,9 +19,17 @@
 int or__layer_view(or_manager *m, int32_t layer, int32_t *active, int32_t *num_cached, int32_t *n_pages,
                    const int32_t **k_ids, const int32_t **v_ids, or_block_pool **kp, or_block_pool **vp);
 
-int or_paged_attend(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *out, int32_t batch,
-                    int32_t n_q_heads, int32_t seq_len, int32_t head_dim, int32_t n_kv_heads,
-                    int32_t n_kv_groups, float scale, int causal) {
+/* to_f32_rt / from_f32_rt for the two 16-bit types (dtype_traits.hpp:52-69) */
+static inline float elem_to_f32(int32_t dtype, uint16_t x) {
+    return dtype == OR_DTYPE_F16 ? or_f16_to_f32(x) : or_bf16_to_f32(x);
+}
+static inline uint16_t elem_from_f32(int32_t dtype, float f) {
+    return dtype == OR_DTYPE_F16 ? or_f32_to_f16(f) : or_f32_to_bf16(f);
+}
+
+int or_paged_attend_dt(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *out, int32_t batch,
+                       int32_t n_q_heads, int32_t seq_len, int32_t head_dim, int32_t n_kv_heads,
+                       int32_t n_kv_groups, float scale, int causal, int32_t dtype) {
     int32_t active, total_cached, num_blocks;
     const int32_t *k_ids, *v_ids;
     or_block_pool *kp, *vp;
@@ -49,20 +58,20 @@ int or_paged_attend(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *o
                         size_t off = ((size_t)t * n_kv_heads + kv_h) * head_dim;
                         float score = 0.0f;
                         for (int32_t d = 0; d < head_dim; ++d)
-                            score += or_bf16_to_f32(qrow[d]) * or_bf16_to_f32(kb[off + d]);
+                            score += elem_to_f32(dtype, qrow[d]) * elem_to_f32(dtype, kb[off + d]);
                         score *= scale;
                         float m_prev = mx;
                         mx = fmaxf(mx, score);
                         float e_s = expf(score - mx);
                         float e_p = expf(m_prev - mx);
                         for (int32_t d = 0; d < head_dim; ++d)
-                            o[d] = o[d] * e_p + e_s * or_bf16_to_f32(vb[off + d]);
+                            o[d] = o[d] * e_p + e_s * elem_to_f32(dtype, vb[off + d]);
                         l = l * e_p + e_s;
                     }
                 }
                 float inv_l = 1.0f / l;
                 uint16_t *orow = out + (((size_t)b * n_q_heads + h) * seq_len + sq) * head_dim;
-                for (int32_t d = 0; d < head_dim; ++d) orow[d] = or_f32_to_bf16(o[d] * inv_l);
+                for (int32_t d = 0; d < head_dim; ++d) orow[d] = elem_from_f32(dtype, o[d] * inv_l);
             }
         }
     }
@@ -70,14 +79,29 @@ int or_paged_attend(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *o
     return 0;
 }
 
+int or_paged_attend(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *out, int32_t batch,
+                    int32_t n_q_heads, int32_t seq_len, int32_t head_dim, int32_t n_kv_heads,
+                    int32_t n_kv_groups, float scale, int causal) {
+    return or_paged_attend_dt(m, layer, Q, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads, n_kv_groups,
+                              scale, causal, OR_DTYPE_BF16);
+}
+
+int or_paged_attention_dt(or_manager *m, int32_t layer, const uint16_t *Q, const uint16_t *K,
+                          const uint16_t *V, uint16_t *out, int32_t batch, int32_t n_q_heads,
+                          int32_t seq_len, int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups,
+                          float scale, int causal, int32_t dtype) {
+    if (!m || !or_mgr_is_active(m, layer)) return 1; /* :124-127 */
+    or_mgr_append_kv_from_tensor(m, layer, K, V, n_kv_heads, seq_len, head_dim, dtype); /* :146 */
+    return or_paged_attend_dt(m, layer, Q, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads, n_kv_groups,
+                              scale, causal, dtype);
+}
+
 int or_paged_attention(or_manager *m, int32_t layer, const uint16_t *Q, const uint16_t *K,
                        const uint16_t *V, uint16_t *out, int32_t batch, int32_t n_q_heads,
                        int32_t seq_len, int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups,
                        float scale, int causal) {
-    if (!m || !or_mgr_is_active(m, layer)) return 1; /* :124-127 */
-    or_mgr_append_kv_from_tensor(m, layer, K, V, n_kv_heads, seq_len, head_dim, OR_DTYPE_BF16); /* :146 */
-    return or_paged_attend(m, layer, Q, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads, n_kv_groups,
-                           scale, causal);
+    return or_paged_attention_dt(m, layer, Q, K, V, out, batch, n_q_heads, seq_len, head_dim, n_kv_heads,
+                                 n_kv_groups, scale, causal, OR_DTYPE_BF16);
 }
 
 /* FlashAttentionImpl<CPU> -- attention.cpp:39-121.  Scores for all keys, causal

@@ -48,6 +48,10 @@ extern "C" {
 #define OR_DTYPE_F16 1
 #define OR_DTYPE_BF16 30
 
+/* ---- fp16 scalar conversion: include/utils/float16.hpp:16-77 (float16_t) ---- */
+uint16_t or_f32_to_f16(float f);
+float or_f16_to_f32(uint16_t h);
+
 /* ---- bf16 scalar conversion: include/utils/bfloat16.hpp:18-45 ---- */
 uint16_t or_f32_to_bf16(float f);
 float or_bf16_to_f32(uint16_t b);
@@ -124,6 +128,16 @@ int or_paged_attention(or_manager *m, int32_t layer, const uint16_t *Q, const ui
 int or_paged_attend(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *out, int32_t batch,
                     int32_t n_q_heads, int32_t seq_len, int32_t head_dim, int32_t n_kv_heads,
                     int32_t n_kv_groups, float scale, int causal);
+/* the same two with the element type of Q, the pools and out (the reference
+ * reads K/V as Q->dtype through to_f32_rt and stores out through from_f32_rt,
+ * dtype_traits.hpp:52-69): OR_DTYPE_BF16 or OR_DTYPE_F16 */
+int or_paged_attention_dt(or_manager *m, int32_t layer, const uint16_t *Q, const uint16_t *K,
+                          const uint16_t *V, uint16_t *out, int32_t batch, int32_t n_q_heads,
+                          int32_t seq_len, int32_t head_dim, int32_t n_kv_heads, int32_t n_kv_groups,
+                          float scale, int causal, int32_t dtype);
+int or_paged_attend_dt(or_manager *m, int32_t layer, const uint16_t *Q, uint16_t *out, int32_t batch,
+                       int32_t n_q_heads, int32_t seq_len, int32_t head_dim, int32_t n_kv_heads,
+                       int32_t n_kv_groups, float scale, int causal, int32_t dtype);
 
 /* ---- FlashAttentionImpl<CPU>::execute: attention.cpp:39-121 (bf16 Q/K/V/out) ---- */
 void or_flash_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *out,

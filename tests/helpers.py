@@ -58,3 +58,25 @@ def oracle_fragmented(orc, Hkv, D, pool, perm_k, perm_v, layer=0, m=None):
 
 def scale_for(D):
     return 1.0 / math.sqrt(D)
+
+
+def f16(bits):
+    return np.ascontiguousarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+# fp16 outputs (10-bit mantissa; probabilities rounded to fp16 in the MFMAs)
+ATTN_F16_MAX_ABS_FRAC = 2.0 ** -8
+ATTN_F16_REL_L2 = 4e-3
+
+
+def assert_attn_close_f16(got_bits, want_bits, label=""):
+    g = f16(got_bits).astype(np.float64)
+    w = f16(want_bits).astype(np.float64)
+    max_abs = float(np.max(np.abs(g - w)))
+    rel_l2 = float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30))
+    ref_max = float(np.max(np.abs(w)))
+    print(f"[{label}] fp16 max_abs={max_abs:.3e} (bound {ATTN_F16_MAX_ABS_FRAC * ref_max:.3e}) rel_l2={rel_l2:.3e}",
+          flush=True)
+    assert np.all(np.isfinite(g)), f"{label}: non-finite output"
+    assert max_abs <= ATTN_F16_MAX_ABS_FRAC * ref_max, f"{label}: max_abs {max_abs}"
+    assert rel_l2 <= ATTN_F16_REL_L2, f"{label}: rel_l2 {rel_l2}"

@@ -459,6 +459,89 @@ def test_paged_attention_gqa_head_map(orc):
     assert np.array_equal(out2[0][[2, 3, 0, 1, 4, 5]], outs[0])
 
 
+# ------------------------------------------------------------------ fp16
+def test_f16_to_f32_all_patterns(orc):
+    """float16_t -> float (float16.hpp:54-77) for all 65536 bit patterns: every
+    non-NaN value equals numpy's exact widening; a NaN becomes sign | 0x7F800000
+    | 0x400000 (the reference keeps only the quiet bit)."""
+    h = np.arange(65536, dtype=np.uint16)
+    got = orc.f16_to_f32(h).view(np.uint32)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(got[~nan], want[~nan].view(np.uint32))
+    sign = (h[nan].astype(np.uint32) >> 15) << 31
+    assert np.array_equal(got[nan], sign | np.uint32(0x7FC00000))
+    assert nan.sum() == 2 * 1023
+
+
+def test_f32_to_f16_matches_nearest_even(orc):
+    """float -> float16_t (float16.hpp:16-51) against numpy's round-to-nearest-even
+    narrowing with gradual underflow: random magnitudes from fp32 subnormals to
+    past fp16 overflow, every halfway point between neighbouring fp16 values
+    near 1, 2^-14 (the subnormal boundary) and 65504, and the specials.  One
+    deliberate difference of the reference: a NaN becomes an infinity of its
+    sign."""
+    rng = np.random.default_rng(1234)
+    mag = np.exp2(rng.uniform(-30.0, 17.0, 200000)).astype(np.float32)
+    x = np.concatenate([mag, -mag, rng.standard_normal(50000).astype(np.float32)])
+    ties = []
+    for base in (1.0, 2.0 ** -14, 2.0 ** -20, 65504.0 / 2.0):
+        b = np.float16(base)
+        for _ in range(64):
+            nb = np.nextafter(b, np.float16(np.inf))
+            ties.append((np.float64(b) + np.float64(nb)) / 2)
+            b = nb
+    specials = [0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e-45, -1e-45, 2.0 ** -24, 2.0 ** -25,
+                3 * 2.0 ** -26, np.inf, -np.inf]
+    x = np.concatenate([x, np.array(ties, dtype=np.float32), np.array(specials, dtype=np.float32)])
+    got = orc.f32_to_f16(x)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    nans = np.array([np.nan, -np.nan], dtype=np.float32)
+    nans[1] = -np.abs(nans[1])
+    assert list(orc.f32_to_f16(nans)) == [0x7C00, 0xFC00]
+
+
+def run_paged_f16(orc, Hq, Hkv, D, chunks, pool=16, seed=0):
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D)
+    m = orc.Manager(with_pool=True)
+    m.init_layer(0, Hkv, D, orc.F16)
+    m.reserve_layer(0, pool)
+    Ks, Vs, outs, qs = [], [], [], []
+    for i, S in enumerate(chunks):
+        q = synth.normal_f16(seed + 10 + i, (1, Hq, S, D))
+        K = synth.normal_f16(seed + 30 + i, (1, Hkv, S, D))
+        V = synth.normal_f16(seed + 50 + i, (1, Hkv, S, D))
+        out, rc = m.paged_attention(0, q, K, V, G, scale, True, dtype=orc.F16)
+        assert rc == 0
+        Ks.append(K[0]), Vs.append(V[0]), qs.append(q[0]), outs.append(out[0])
+    return m, qs, Ks, Vs, outs, scale
+
+
+def h64(bits):
+    return bits.view(np.float16).astype(np.float64)
+
+
+@pytest.mark.parametrize("chunks", [[1], [9], [20, 1, 1]])
+def test_paged_attention_f16_bruteforce(orc, chunks):
+    """The op on an fp16 layer (K/V read as Q's dtype, attention.cpp:186-200;
+    out through float16_t) against fp64 softmax(q K^T scale) V; a single key
+    gives exactly v."""
+    Hq, Hkv, D = 4, 2, 32
+    m, qs, Ks, Vs, outs, scale = run_paged_f16(orc, Hq, Hkv, D, chunks, seed=600)
+    n = 0
+    for q, o, S in zip(qs, outs, chunks):
+        n += S
+        K = h64(np.concatenate(Ks, axis=1)[:, :n])
+        V = h64(np.concatenate(Vs, axis=1)[:, :n])
+        want = brute_attention(h64(q), K, V, Hq // Hkv, scale, True, n)
+        assert np.max(np.abs(h64(o) - want)) <= 2.0 ** -10 * np.max(np.abs(want)) + 1e-4
+    if chunks == [1]:
+        assert np.array_equal(outs[0][0::2, 0], Vs[0][:, 0]) and np.array_equal(outs[0][1::2, 0], Vs[0][:, 0])
+
+
 def test_paged_attention_inactive_layer_untouched(orc):
     m = orc.Manager(with_pool=True)
     q = synth.normal_bf16(1, (1, 2, 1, 16))
