@@ -21,7 +21,8 @@ exceed the op step's time; the bench exits with an error if it does.  Its HBM
 traffic is measured in the same run: two child rocprofv3 --pmc passes
 (FETCH_SIZE, WRITE_SIZE) over the same launches and a 256 MiB copy that scales
 the counters, started before this process touches the GPU.
-Secondary figures (same line): config 2 fused append GB/s, config 4 causal
+Secondary figures (same line): the headline op step on fp16 layers, config 2
+fused append GB/s, config 4 causal
 prefill TFLOPS, the non-paged FlashAttention path at config 4's shape, the
 Qwen3.5 shape (head_dim 256, 8 q / 2 kv heads: 8K-context decode GB/s and
 2048-token prefill TFLOPS), config 5 36-layer long-context decode (eager and
@@ -29,7 +30,7 @@ replayed as one HIP graph), and the Qwen3-4B fused Q/K/V projection feeding
 the path (decode GEMV GB/s, 2048-token GEMM TFLOPS).  cpu_baseline = the
 oracle (single thread) on a bounded sample of the headline workload.
 
---only {headline,append,prefill,flash,qwen35,longctx,linear,copy,traffic,
+--only {headline,f16,append,prefill,flash,qwen35,longctx,linear,copy,traffic,
 prefill_scale,decode_scale} runs one workload alone (for rocprofv3 passes);
 the line then carries only that workload's figures.  prefill_scale (the
 prefill kernel at 2K-16K tokens) and decode_scale (the decode kernels at
@@ -67,8 +68,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=16, help="rotation depth of the headline workload")
-    ap.add_argument("--only", choices=["headline", "append", "prefill", "flash", "qwen35", "longctx", "linear", "copy",
-                                       "traffic", "prefill_scale", "decode_scale"], default=None)
+    ap.add_argument("--only", choices=["headline", "f16", "append", "prefill", "flash", "qwen35", "longctx", "linear",
+                                       "copy", "traffic", "prefill_scale", "decode_scale"], default=None)
     ap.add_argument("--no-traffic", action="store_true", help="skip the child rocprofv3 --pmc traffic passes")
     ap.add_argument("--skip-secondary", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -175,26 +176,63 @@ DECODE_KERNEL_LABEL = ("paged_decode_kernel<128, 8> (split-K attention, split me
                        "then the log-sum-exp merge of the splits)")
 
 
-def decode_layers(np, torch, paged, synth, call, L):
+def decode_layers(np, torch, paged, synth, call, L, f16=False):
     """L Qwen3-4B-shape layers of config 3: 8192 cached tokens each in a
-    shuffled 2048-page pool, pools ~ N(0,1), and per layer a q, k, v of one token."""
+    shuffled 2048-page pool, pools ~ N(0,1), and per layer a q, k, v of one
+    token; bf16 layers, or fp16 layers with f16."""
     Hq, Hkv, D, pool_pages, n0 = HQ3, HKV3, D3, POOL3, N3
     seed = synth.config_seed(3)
+    fill = "genllm_fill_normal_f16" if f16 else "genllm_fill_normal_bf16"
+    gen = synth.normal_f16 if f16 else synth.normal_bf16
+    dev = paged.to_device_f16 if f16 else paged.to_device_bf16
     mgr = paged.PagedAttentionManager(L * 2 * pool_pages * PAGE * Hkv * D * 2)
     for l in range(L):
-        mgr.init_layer(l, Hkv, D)
+        mgr.init_layer(l, Hkv, D, paged.DTYPE_F16 if f16 else paged.DTYPE_BF16)
         mgr.reserve_layer(l, pool_pages)
         mgr.fragment(l, synth.shuffled(seed + 2 * l, pool_pages), synth.shuffled(seed + 2 * l + 1, pool_pages))
         mgr.append_kv_pages(l, n0)
         info = mgr.get_layer(l)
         n_el = pool_pages * PAGE * Hkv * D
-        call("genllm_fill_normal_bf16", info.k_pool, n_el, seed + 100 + l, 0, None)
-        call("genllm_fill_normal_bf16", info.v_pool, n_el, seed + 200 + l, 0, None)
-    q = [paged.to_device_bf16(synth.normal_bf16(seed + 300 + l, (1, Hq, 1, D))) for l in range(L)]
-    kn = [paged.to_device_bf16(synth.normal_bf16(seed + 400 + l, (1, Hkv, 1, D))) for l in range(L)]
-    vn = [paged.to_device_bf16(synth.normal_bf16(seed + 500 + l, (1, Hkv, 1, D))) for l in range(L)]
+        call(fill, info.k_pool, n_el, seed + 100 + l, 0, None)
+        call(fill, info.v_pool, n_el, seed + 200 + l, 0, None)
+    q = [dev(gen(seed + 300 + l, (1, Hq, 1, D))) for l in range(L)]
+    kn = [dev(gen(seed + 400 + l, (1, Hkv, 1, D))) for l in range(L)]
+    vn = [dev(gen(seed + 500 + l, (1, Hkv, 1, D))) for l in range(L)]
     torch.cuda.synchronize()
     return mgr, q, kn, vn, seed
+
+
+def time_op_steps(torch, op_step, args):
+    """The op step timed two ways.  host_loop_s: wall clock around the steps
+    issued one after another from Python (host in the loop; labelled, not the
+    value).  step_s: one HIP event pair on the launch stream around the same
+    number of further steps, queued while a bounded spin kernel holds the GPU,
+    so that it never waits for the host (as the roofline kernel is timed);
+    queue_s is the host time per call meanwhile.  op_step(i) returns the
+    step's algorithmic bytes; total_bytes is the sum over the event-timed
+    steps.  Returns (host_loop_s, step_s, queue_s, total_bytes)."""
+    for i in range(args.warmup):
+        op_step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        op_step(args.warmup + i)
+    torch.cuda.synchronize()
+    host_loop_s = (time.perf_counter() - t0) / args.steps
+    base = args.warmup + args.steps
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.4e9 * max(0.002, 3.0 * args.steps * (host_loop_s + 20e-6))))
+    start.record(stream)
+    total_bytes = 0
+    q0 = time.perf_counter()
+    for i in range(args.steps):
+        total_bytes += op_step(base + i)
+    queue_s = (time.perf_counter() - q0) / args.steps
+    stop.record(stream)
+    torch.cuda.synchronize()
+    step_s = 1e-3 * start.elapsed_time(stop) / args.steps
+    return host_loop_s, step_s, queue_s, total_bytes
 
 
 def decode_launcher(np, torch, paged, mgr, q, L):
@@ -230,36 +268,12 @@ def headline(args, np, torch, paged, synth, call):
         cached[l] += 1
         return decode_step_bytes(cached[l])
 
-    for i in range(args.warmup):
-        op_step(i)
-    torch.cuda.synchronize()
-    # The op step with the host in the loop: wall clock around the steps as a
-    # caller issuing one step after another sees it (labelled, not the value).
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        op_step(args.warmup + i)
-    torch.cuda.synchronize()
-    host_loop_s = (time.perf_counter() - t0) / args.steps
-    # The op step on the GPU (value, ms_per_step): one HIP event pair on the
-    # launch stream around the timed steps, queued while a bounded spin
-    # kernel holds the GPU, so that it never waits for the host (as the
-    # roofline kernel is timed).  Bytes are those of exactly these steps.
-    base = args.warmup + args.steps
-    stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(int(2.4e9 * max(0.002, 3.0 * args.steps * (host_loop_s + 20e-6))))
-    start.record(stream)
-    total_bytes = 0
-    q0 = time.perf_counter()
-    for i in range(args.steps):
-        total_bytes += op_step(base + i)
-    queue_s = (time.perf_counter() - q0) / args.steps
-    stop.record(stream)
-    torch.cuda.synchronize()
-    step_s = 1e-3 * start.elapsed_time(stop) / args.steps
+    # value and ms_per_step: the GPU time of the op step; the wall clock of the
+    # host loop beside it
+    host_loop_s, step_s, queue_s, total_bytes = time_op_steps(torch, op_step, args)
 
-    # dominant kernel alone: split-K decode with its in-launch merge, 8193 keys,
-    # rotating over the same 16 layers
+    # dominant kernels alone: the split-K decode and its merge kernel, 8193
+    # keys, rotating over the same 16 layers
     kernel_launch, n_keys = decode_launcher(np, torch, paged, mgr, q, L)
     n_k = max(args.steps, 200)
     k_mean = time_kernels(torch, kernel_launch, n_k, warm=args.warmup)
@@ -312,6 +326,30 @@ def headline(args, np, torch, paged, synth, call):
 
 
 # ---------------------------------------------------------------- secondary
+def f16_config3(args, np, torch, paged, synth, call):
+    """The headline op step on fp16 layers (fp16 K/V pools, q and out): the
+    same shape, rotation and timing, the fp16 MFMAs in the split kernel."""
+    Hq, Hkv, D, L = HQ3, HKV3, D3, args.layers
+    G, scale = Hq // Hkv, 1.0 / np.sqrt(D)
+    mgr, q, kn, vn, _ = decode_layers(np, torch, paged, synth, call, L, f16=True)
+    out = [torch.empty((1, Hq, 1, D), dtype=torch.float16, device="cuda") for _ in range(L)]
+    cached = [N3] * L
+
+    def op_step(i):
+        l = i % L
+        paged.paged_attention(mgr, l, q[l], kn[l], vn[l], out[l], G, scale)
+        cached[l] += 1
+        return decode_step_bytes(cached[l])
+
+    host_loop_s, step_s, _, total_bytes = time_op_steps(torch, op_step, args)
+    mgr.close()
+    gbs = total_bytes / (step_s * args.steps) / 1e9
+    return {"us_per_step": round(step_s * 1e6, 3), "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "host_loop_us_per_step": round(host_loop_s * 1e6, 2), "dtype": "f16",
+            "workload": "config 3 op step (append 1 token, attend over 8193+ keys) on fp16 layers, "
+                        f"{L} rotating layers, timed as the headline"}
+
+
 def append_cfg2(np, torch, paged, synth, call):
     S, Hkv, D, pool = 4096, 8, 128, 1024
     seed = synth.config_seed(2)
@@ -883,6 +921,9 @@ def main():
     if args.only == "traffic":
         print(json.dumps({"only": args.only, **traffic_workload(args, *common)}), flush=True)
         return
+    if args.only == "f16":
+        print(json.dumps({"only": args.only, **f16_config3(args, *common)}), flush=True)
+        return
     if args.only and args.only != "headline":
         fn = {"append": append_cfg2, "prefill": prefill_cfg4, "flash": flash_cfg4, "qwen35": qwen35_d256,
               "longctx": longctx_cfg5, "linear": linear_qkv, "copy": copy_calibration,
@@ -926,7 +967,8 @@ def main():
     if not args.skip_secondary and not args.only:
         result["secondary"] = {"append_config2": append_cfg2(*common), "prefill_config4": prefill_cfg4(*common),
                                "flash_config4": flash_cfg4(*common), "qwen35_head_dim_256": qwen35_d256(*common),
-                               "longctx_config5": longctx_cfg5(*common), "linear_qkv_4b": linear_qkv(*common)}
+                               "longctx_config5": longctx_cfg5(*common), "linear_qkv_4b": linear_qkv(*common),
+                               "f16_config3": f16_config3(args, *common)}
         # read floors (probes that move each kernel's bytes with its access
         # pattern and no arithmetic), next to the kernels they bound
         sec = result["secondary"]

@@ -108,6 +108,7 @@ SIGNATURES = {
     "genllm_linear_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "genllm_linear": (_int, [_P, _P, _P, _P, _i64, _i64, _i64, _P, _sz, _P]),
     "genllm_fill_normal_bf16": (_int, [_P, _sz, _u64, _u64, _P]),
+    "genllm_fill_normal_f16": (_int, [_P, _sz, _u64, _u64, _P]),
     "genllm_selftest_mfma": (_int, [_i32, _P, _P, _P, _P]),
 }
 

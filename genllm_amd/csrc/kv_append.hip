@@ -35,6 +35,8 @@
 //   pool + id[g/16]*page_elems + (g%16)*Hkv*D + h*D        (page layout [16][Hkv][D])
 // Ids of pages opened by this call may come in the launch arguments (decode
 // opens at most one page); block 0 also writes them into the device table.
+#include <cstddef>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -308,6 +310,9 @@ struct Append {
 
 template <int D, int TR>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
+    // the scalar fields and the table-update header; the opened pages' ids
+    // that follow are read per lane where needed
+    prefetch_kernargs<offsetof(AppendParams, upd) + 2 * sizeof(int32_t)>();
     Append<D, TR>::run(p);
 }
 

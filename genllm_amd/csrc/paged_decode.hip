@@ -227,6 +227,7 @@ __device__ __forceinline__ int step_load(const int32_t* at) {
 template <int D, int W, bool kStep, bool F16>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     using E = Elem<F16>;
+    prefetch_kernargs<sizeof(AttnParams)>();
     static_assert(D == 128 || D == 256, "decode kernel: head_dim 128 or 256");
     constexpr int KS = D / 32;   // S^T k-steps
     constexpr int DB = D / 16;   // O^T dim blocks
@@ -632,6 +633,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 // Qwen3.5 shape, on a box where config 3 took 13.6).
 template <int D, int MW, bool F16>
 __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams p) {
+    prefetch_kernargs<sizeof(AttnParams)>();
     constexpr int U = kMergeU;  // splits in flight per lane
     constexpr int PL = 1;       // dims per lane (the workgroup's kMergeDims dims)
     static_assert(kMergeDims == 64 * PL, "merge: one lane per dim group");

@@ -8,14 +8,15 @@ namespace genllm {
 
 // Counter-based normal generator: h = mix64(seed + i * golden), two 24-bit
 // uniforms u1 in (0,1], u2 in [0,1), z = sqrt(-2 ln u1) cos(2 pi u2) in fp32,
-// rounded to bf16 like bfloat16_t (RNE).  genllm_amd/synth.py computes the same
-// formula on the host.
+// rounded to bf16 like bfloat16_t or to fp16 like float16_t (RNE).
+// genllm_amd/synth.py computes the same formula on the host.
 __device__ __forceinline__ uint64_t mix64(uint64_t x) {
     x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
     x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
     return x ^ (x >> 31);
 }
 
+template <bool F16>
 __global__ void fill_normal_kernel(uint16_t* dst, size_t n, uint64_t seed, uint64_t offset) {
     const size_t stride = size_t(gridDim.x) * blockDim.x;
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -24,7 +25,7 @@ __global__ void fill_normal_kernel(uint16_t* dst, size_t n, uint64_t seed, uint6
         const float u2 = float((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
         const float r = sqrtf(-2.0f * logf(u1));
         const float z = r * cosf(6.2831853071795864f * u2);
-        dst[i] = uint16_t(f32_to_bf16_ref(z));
+        dst[i] = uint16_t(F16 ? f32_to_f16_ref(z) : f32_to_bf16_ref(z));
     }
 }
 
@@ -59,14 +60,25 @@ __global__ void selftest_mfma_kernel(const uint16_t* a, const uint16_t* b, float
 
 using namespace genllm;
 
-extern "C" int genllm_fill_normal_bf16(void* dst, size_t n, uint64_t seed, uint64_t offset, void* stream) {
+namespace {
+template <bool F16>
+int fill_normal(void* dst, size_t n, uint64_t seed, uint64_t offset, void* stream) {
     if (n == 0) return GENLLM_OK;
     if (!dst) return fail(GENLLM_ERR_INVALID, "fill_normal: null dst");
     const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
-    hipLaunchKernelGGL(fill_normal_kernel, dim3(unsigned(blocks)), dim3(256), 0, as_stream(stream),
+    hipLaunchKernelGGL(fill_normal_kernel<F16>, dim3(unsigned(blocks)), dim3(256), 0, as_stream(stream),
                        static_cast<uint16_t*>(dst), n, seed, offset);
     GENLLM_LAUNCH_CHECK("fill_normal_kernel");
     return GENLLM_OK;
+}
+}  // namespace
+
+extern "C" int genllm_fill_normal_bf16(void* dst, size_t n, uint64_t seed, uint64_t offset, void* stream) {
+    return fill_normal<false>(dst, n, seed, offset, stream);
+}
+
+extern "C" int genllm_fill_normal_f16(void* dst, size_t n, uint64_t seed, uint64_t offset, void* stream) {
+    return fill_normal<true>(dst, n, seed, offset, stream);
 }
 
 extern "C" int genllm_selftest_mfma(int32_t k, const void* a, const void* b, float* c, void* stream) {

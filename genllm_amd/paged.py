@@ -127,11 +127,13 @@ class PagedAttentionManager:
         call("genllm_kv_append_pages", self._h, layer, count, _stream(stream))
 
     def append_kv_from_pos(self, layer: int, k, v, global_pos: int, stream=None):
-        """append_kv_from_pos: k, v device bf16 head-major [Hkv][count][D]."""
+        """append_kv_from_pos: k, v device head-major [Hkv][count][D], bf16 or
+        fp16 as the layer's pools (the library refuses another type)."""
         Hkv, count, D = k.shape
         for t in (k, v):
-            assert t.dtype == torch.bfloat16 and t.is_contiguous()
-        call("genllm_kv_append_from_pos", self._h, layer, _ptr(k), _ptr(v), Hkv, D, DTYPE_BF16, global_pos, count,
+            assert t.dtype in (torch.bfloat16, torch.float16) and t.dtype == k.dtype and t.is_contiguous()
+        dtype = DTYPE_F16 if k.dtype == torch.float16 else DTYPE_BF16
+        call("genllm_kv_append_from_pos", self._h, layer, _ptr(k), _ptr(v), Hkv, D, dtype, global_pos, count,
              _stream(stream))
 
     def reset(self):
@@ -401,6 +403,10 @@ def fill_normal_bf16(t: torch.Tensor, seed: int, offset: int = 0, stream=None):
     call("genllm_fill_normal_bf16", _ptr(t), t.numel(), seed, offset, _stream(stream))
 
 
+def fill_normal_f16(t: torch.Tensor, seed: int, offset: int = 0, stream=None):
+    call("genllm_fill_normal_f16", _ptr(t), t.numel(), seed, offset, _stream(stream))
+
+
 def selftest_mfma(a, b, c, stream=None):
     """a [16][k], b [k][16] bf16 (k = 32 or 16) -> c [16][16] fp32 via one MFMA."""
     call("genllm_selftest_mfma", a.shape[1], _ptr(a), _ptr(b), _ptr(c), _stream(stream))
@@ -424,6 +430,7 @@ def to_host_bits(t: torch.Tensor) -> np.ndarray:
 __all__ = [
     "PagedAttentionManager", "paged_attention", "qk_norm_rope_append", "rms_norm", "apply_rope", "rope_cache",
     "kv_scatter", "paged_decode", "paged_decode_noalloc", "paged_prefill", "flash_attention", "decode_workspace_bytes", "fill_normal_bf16",
+    "fill_normal_f16",
     "selftest_mfma", "device_view", "to_device_bf16", "to_device_f16", "to_host_bits", "GenllmError", "PAGE",
     "DTYPE_BF16", "DTYPE_F16",
 ]

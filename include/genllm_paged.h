@@ -327,8 +327,10 @@ int genllm_linear(const void *x, const void *w, const void *bias, void *out, int
 
 /* ------------------------------------------------------------ utilities
  * No counterpart in the reference: synthetic seeded inputs for tests and the
- * benchmark (counter-based hash -> Box-Muller -> RNE bf16). */
+ * benchmark (counter-based hash -> Box-Muller -> RNE bf16, or RNE fp16 with
+ * gradual underflow). */
 int genllm_fill_normal_bf16(void *dst, size_t n, uint64_t seed, uint64_t offset, void *stream);
+int genllm_fill_normal_f16(void *dst, size_t n, uint64_t seed, uint64_t offset, void *stream);
 
 /* No counterpart in the reference: runs one bf16 MFMA, k = 32
  * (v_mfma_f32_16x16x32_bf16) or k = 16 (v_mfma_f32_16x16x16_bf16), on

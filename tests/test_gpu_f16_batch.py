@@ -152,3 +152,17 @@ def test_batch2_entries_share_the_cache(orc, f16):
         step(orc, mgr, ref, Hq, Hkv, 1, D, 600 + 3 * i, f"batch2 decode {41 + i}", f16=f16, batch=2)
     check_pools(mgr, ref, "batch2")
     mgr.close()
+
+
+def test_fill_normal_f16_matches_host_formula():
+    """genllm_fill_normal_f16 (the benchmark's fp16 pools) against the host
+    formula of genllm_amd/synth.py: the same samples within one fp16 rounding
+    of each other (device and numpy libm differ by a few fp32 ulps)."""
+    t = torch.empty(1 << 16, dtype=torch.float16, device="cuda")
+    paged.fill_normal_f16(t, 1234, 77)
+    torch.cuda.synchronize()
+    got = paged.to_host_bits(t).view(np.float16).astype(np.float64)
+    want = synth.normal_f16(1234, (1 << 16,), 77).view(np.float16).astype(np.float64)
+    ulp = np.maximum(np.abs(want), 2.0 ** -14) * 2.0 ** -10
+    assert np.all(np.abs(got - want) <= ulp), np.max(np.abs(got - want) / ulp)
+    assert abs(want.mean()) < 0.02 and abs(want.std() - 1) < 0.02
