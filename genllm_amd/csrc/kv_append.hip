@@ -31,6 +31,15 @@
 // V lanes: lane j copies elements 8j + 64u + {0..7} (16-byte loads/stores,
 // 128 contiguous bytes per row per instruction); V is never rounded: bit-exact.
 //
+// gamma: every q and K wave needs the same D floats.  Loaded by every wave,
+// they are the same few cache lines requested by about a thousand waves per
+// XCD at kernel start, and those requests queue on the L2 channels that hold
+// them (config 2: 7.14 us with gamma taken as a constant, 7.51-7.53 us loaded
+// per wave).  Here one wave per workgroup of kBlockWaves loads each gamma and
+// stages it in LDS; every wave reads it after one barrier, met once its own
+// loads are in flight (7.32-7.34 us with 8-wave workgroups; 4 waves 7.40-7.52,
+// 16 waves 7.98 us; A/B on one box, two passes each).
+//
 // Page address of token t (global position g = pos0 + t):
 //   pool + id[g/16]*page_elems + (g%16)*Hkv*D + h*D        (page layout [16][Hkv][D])
 // Ids of pages opened by this call may come in the launch arguments (decode
@@ -52,6 +61,7 @@ namespace genllm {
 namespace {
 
 constexpr int TPW = 1;  // tasks per wave (measured at config 2: 1 and 2 beat 4; 8 is 1.5x slower than 4)
+constexpr int kBlockWaves = 8;  // waves per workgroup, sharing one staged copy of each gamma
 
 // TR = rope_dim / 64: chunk t < TR of a lane rotates with chunk t + TR (the
 // pair (i, i + rope_dim/2)); chunks from 2 TR on pass through.  TR = D/64 is
@@ -164,6 +174,7 @@ struct Append {
     }
 
     __device__ static void run(const AppendParams& p) {
+        __shared__ __attribute__((aligned(16))) float s_gamma[2][D];  // gamma_q, gamma_k of the workgroup
         const int lane = threadIdx.x & 63;
         const int r = lane >> 3, j = lane & 7;
         if (blockIdx.x == 0 && threadIdx.x < p.upd.count) {
@@ -178,7 +189,28 @@ struct Append {
         // pointers are then chosen in scalar registers, not by per-lane selects
         // that turn kernel-argument reads into vector loads (and a wait for
         // every load in flight)
-        int64_t w = int64_t(blockIdx.x) * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        int64_t w = int64_t(blockIdx.x) * kBlockWaves + wv;
+        // Wave 0 loads gamma_q if the workgroup holds q tasks, wave 1 gamma_k if
+        // it holds K tasks, first of all their loads; stage_gamma, called exactly
+        // once by every wave, stores them to LDS and meets the barrier.
+        constexpr int GE = D / 64;  // gamma floats per lane
+        const int64_t w_first = int64_t(blockIdx.x) * kBlockWaves, w_last = w_first + kBlockWaves - 1;
+        const float* gsrc = wv == 0 && w_first < wq                      ? p.gamma_q
+                            : wv == 1 && w_first < wq + wk && w_last >= wq ? p.gamma_k
+                                                                           : nullptr;
+        float gst[GE];
+        if (gsrc) {
+#pragma unroll
+            for (int e = 0; e < GE; ++e) gst[e] = gsrc[GE * lane + e];
+        }
+        auto stage_gamma = [&]() {
+            if (gsrc) {
+#pragma unroll
+                for (int e = 0; e < GE; ++e) s_gamma[wv][GE * lane + e] = gst[e];
+            }
+            __syncthreads();
+        };
         int kind;
         int64_t t0, n_kind;
         int ng;
@@ -188,7 +220,10 @@ struct Append {
             kind = 1, t0 = (w - wq) * TPW, n_kind = nk, ng = ngk;
         } else {
             kind = 2, t0 = (w - wq - wk) * TPW, n_kind = nk, ng = ngk;
-            if (t0 >= n_kind) return;
+            if (t0 >= n_kind) {
+                stage_gamma();
+                return;
+            }
         }
 
         if (kind < 2) {
@@ -196,8 +231,8 @@ struct Append {
             const int H = is_q ? p.Hq : p.Hkv;
             // Every load of the wave is issued before any arithmetic: the K page
             // ids first (the address is formed from the first load to land; the
-            // load counter is in order), then the rows, gamma (once) and the
-            // RoPE table chunks of each row's position.
+            // load counter is in order), then the rows and the RoPE table
+            // chunks of each row's position; gamma comes from LDS.
             uint2 x[TPW][R];
             float4 c4[TPW][TR], s4[TPW][TR];
             int tok[TPW], h[TPW];
@@ -216,10 +251,6 @@ struct Append {
             }
             const float* gamma = is_q ? p.gamma_q : p.gamma_k;
             float4 gw[R];
-            if (gamma) {
-#pragma unroll
-                for (int c = 0; c < R; ++c) gw[c] = *reinterpret_cast<const float4*>(gamma + 4 * j + 32 * c);
-            }
 #pragma unroll
             for (int u = 0; u < TPW; ++u) {
                 const uint16_t* src = is_q ? p.q + tok[u] * p.q_tok_stride + h[u] * p.q_head_stride
@@ -239,6 +270,11 @@ struct Append {
                         s4[u][c] = *reinterpret_cast<const float4*>(p.sin_tab + row + 32 * c);
                     }
                 }
+            }
+            stage_gamma();
+            if (gamma) {
+#pragma unroll
+                for (int c = 0; c < R; ++c) gw[c] = *reinterpret_cast<const float4*>(&s_gamma[is_q ? 0 : 1][4 * j + 32 * c]);
             }
             // the page ids are used only now, with every load of the wave in flight
             uint16_t* dsts[TPW];
@@ -297,6 +333,7 @@ struct Append {
                 const int64_t id = ok ? page_id(p, gpos / kPage, 1) : -1;
                 dst[u] = id >= 0 ? id * p.page_elems + int64_t(gpos % kPage) * p.Hkv * D + hh * D : -1;
             }
+            stage_gamma();
 #pragma unroll
             for (int u = 0; u < TPW; ++u)
                 if (dst[u] >= 0)
@@ -309,7 +346,7 @@ struct Append {
 };
 
 template <int D, int TR>
-__global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
+__global__ __launch_bounds__(kBlockWaves * 64) void kv_append_kernel(AppendParams p) {
     // the scalar fields and the table-update header; the opened pages' ids
     // that follow are read per lane where needed
     prefetch_kernargs<offsetof(AppendParams, upd) + 2 * sizeof(int32_t)>();
@@ -321,7 +358,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
 int launch_kv_append(const AppendParams& p, int head_dim, hipStream_t stream) {
     const int64_t nq = int64_t(p.S) * p.nq_tasks, nk = int64_t(p.S) * p.nkv_tasks;
     const int64_t waves = (nq + TPW - 1) / TPW + 2 * ((nk + TPW - 1) / TPW);
-    int64_t blocks = (waves + 3) / 4;
+    int64_t blocks = (waves + kBlockWaves - 1) / kBlockWaves;
     if (blocks <= 0) {
         if (p.upd.count == 0) return GENLLM_OK;
         blocks = 1;  // table update only
@@ -329,7 +366,7 @@ int launch_kv_append(const AppendParams& p, int head_dim, hipStream_t stream) {
     // rope_dim: the rotated dims (head_dim for the reference's full rotation;
     // without tables it does not matter)
     const int rd = p.cos_tab ? (p.rope_dim ? p.rope_dim : head_dim) : head_dim;
-    const dim3 g{unsigned(blocks)}, b{256u};
+    const dim3 g{unsigned(blocks)}, b{unsigned(kBlockWaves * 64)};
     switch (head_dim * 1000 + rd) {
         case 64 * 1000 + 64: hipLaunchKernelGGL((kv_append_kernel<64, 1>), g, b, 0, stream, p); break;
         case 128 * 1000 + 64: hipLaunchKernelGGL((kv_append_kernel<128, 1>), g, b, 0, stream, p); break;
