@@ -60,6 +60,7 @@ constexpr int kWideWaves = 8;   // waves of a split workgroup over short ranges 
 // for the captured decode step, whose plan covers 65)
 constexpr int kWideMaxPps = 128;
 constexpr int kMergeU = 16;     // splits in flight per merge lane
+constexpr size_t kSplitLeadArgBytes = 56;  // the split kernel's scalar arguments ahead of the parameter block
 constexpr int kMergeDims = 64;  // dims per merge workgroup
 constexpr int kMaxSplits = 256;
 // pages in flight per wave: 1 at D = 128 (a wave requests page j+1 only after
@@ -224,10 +225,17 @@ __device__ __forceinline__ int step_load(const int32_t* at) {
         __hip_atomic_load(const_cast<int32_t*>(at), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
+// The fields the first loads need (block table, split range, the ids opened
+// by this call, q) come first as scalars (14 dwords), ahead of the parameter
+// block, so that they can be preloaded into SGPRs at wave launch: the page-id
+// and q loads then leave without an argument read before them.
 template <int D, int W, bool kStep, bool F16>
-__global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
+__global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_ids, const int32_t* v_ids,
+                                                              const uint16_t* q, int32_t q_head_stride,
+                                                              int32_t q_tok_stride, int32_t G, int32_t S,
+                                                              int32_t pages_per_split, int32_t n_pages_arg,
+                                                              int32_t upd_first, int32_t upd_count, AttnParams p) {
     using E = Elem<F16>;
-    prefetch_kernargs<sizeof(AttnParams)>();
     static_assert(D == 128 || D == 256, "decode kernel: head_dim 128 or 256");
     constexpr int KS = D / 32;   // S^T k-steps
     constexpr int DB = D / 16;   // O^T dim blocks
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n16 = lane & 15, g = lane >> 4;
     const int h = blockIdx.x, sp = blockIdx.y;
-    const int rows_total = p.G * p.S;  // <= 16
+    const int rows_total = G * S;  // <= 16
 
     // q rows and the block-table entries of the wave's planned page range are
     // requested first: neither depends on the cache position, so in a
@@ -254,7 +262,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     const bool row_ok = r < rows_total;
     uint4 qb[KS];  // Q^T operand chunks (raw 16-bit elements)
     {
-        const uint16_t* qrow = p.q + int64_t(h * p.G + r % p.G) * p.q_head_stride + int64_t(r / p.G) * p.q_tok_stride;
+        const uint16_t* qrow = q + int64_t(h * G + r % G) * q_head_stride + int64_t(r / G) * q_tok_stride;
 #pragma unroll
         for (int c = 0; c < KS; ++c) {
             uint4 u = make_uint4(0, 0, 0, 0);
@@ -262,13 +270,13 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
             qb[c] = u;
         }
     }
-    const int begin = sp * p.pages_per_split;
-    const int end_plan = min(begin + p.pages_per_split, p.n_pages);
+    const int begin = sp * pages_per_split;
+    const int end_plan = min(begin + pages_per_split, n_pages_arg);
     const int np_plan = end_plan - begin - wv > 0 ? (end_plan - begin - wv + W - 1) / W : 0;
     // fused append: page ids opened by this call come from the launch arguments
-    if (sp == 0 && h == 0 && threadIdx.x < p.upd.count) {
-        p.k_ids_w[p.upd.first + threadIdx.x] = p.upd.k[threadIdx.x];
-        p.v_ids_w[p.upd.first + threadIdx.x] = p.upd.v[threadIdx.x];
+    if (sp == 0 && h == 0 && threadIdx.x < upd_count) {
+        p.k_ids_w[upd_first + threadIdx.x] = p.upd.k[threadIdx.x];
+        p.v_ids_w[upd_first + threadIdx.x] = p.upd.v[threadIdx.x];
     }
     // Block-table entries of the wave's pages, 64 at a time: lane i holds the
     // ids of the wave's page 64 b + i of id block b.  The current block is in
@@ -282,29 +290,32 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
         const int jj = 64 * b + lane;
         if (jj < np_plan) {
             const int pg = begin + wv + W * jj;
-            const int rel = pg - p.upd.first;
-            if (rel >= 0 && rel < p.upd.count) {
+            const int rel = pg - upd_first;
+            if (rel >= 0 && rel < upd_count) {
                 kid = p.upd.k[rel];
                 vid = p.upd.v[rel];
             } else {
-                kid = p.k_ids[pg];
-                vid = p.v_ids[pg];
+                kid = k_ids[pg];
+                vid = v_ids[pg];
             }
         }
     };
     int my_kid, my_vid, nx_kid = 0, nx_vid = 0;
     fetch_ids(0, my_kid, my_vid);
     if (np_plan > 64) fetch_ids(1, nx_kid, nx_vid);  // wave-uniform
+    // the parameter block's lines, all at once, with the id and q loads already
+    // in flight (the block's reads below then hit the scalar cache)
+    prefetch_kernargs<kSplitLeadArgBytes + sizeof(AttnParams)>();
 
     // Cache position: from the launch arguments, or (device-position step)
     // from the control block, where a step that would pass the staged limit
     // or the pages the grid was planned for only raises the error flag.
-    int n_cached = p.n_cached, n_pages = p.n_pages, new_from = p.new_from, step_pos = 0;
+    int n_cached = p.n_cached, n_pages = n_pages_arg, new_from = p.new_from, step_pos = 0;
     if constexpr (kStep) {
         step_pos = step_load(p.step + kStepPos);
         const int limit = step_load(p.step + kStepLimit);
         if (step_load(p.step + kStepError)) return;  // an earlier kernel of this or a previous step was refused
-        if (step_pos < 0 || step_pos > limit - p.S || (step_pos + p.S + kPage - 1) / kPage > p.n_pages) {
+        if (step_pos < 0 || step_pos > limit - S || (step_pos + S + kPage - 1) / kPage > n_pages_arg) {
             if (threadIdx.x == 0)
                 __hip_atomic_store(p.step + kStepError, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
@@ -315,7 +326,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     }
 
     const int qabs = p.causal ? n_cached - p.S + r / p.G : n_cached - 1;
-    const int end = min(begin + p.pages_per_split, n_pages);
+    const int end = min(begin + pages_per_split, n_pages);
     const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;  // <= np_plan
     // Element offsets inside a page (< 2^31): lane's K operand chunk (token
     // n16, dims 8g + 32c) and V row chunk (token 4g + i, dims 8 n16).  Page
@@ -631,9 +642,15 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 // box, 128-dim blocks against 64: Qwen3.5 (D = 256, 103 splits) 12.8 -> 12.3
 // us per decode, config 3 13.1 -> 12.9 us (whole rows measured 14.2 us on the
 // Qwen3.5 shape, on a box where config 3 took 13.6).
+//
+// The arguments are scalars (14 dwords), not the parameter block, so that they
+// can be preloaded into SGPRs at wave launch: the partial loads then need no
+// argument read before them.  ml_off: float index of {m, l} in the partials.
 template <int D, int MW, bool F16>
-__global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams p) {
-    prefetch_kernargs<sizeof(AttnParams)>();
+__global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(const float* partial, uint16_t* out,
+                                                                     int64_t o_head_stride, int64_t o_tok_stride,
+                                                                     int32_t n_splits, int32_t G, int32_t S,
+                                                                     int32_t ml_off, int32_t* step) {
     constexpr int U = kMergeU;  // splits in flight per lane
     constexpr int PL = 1;       // dims per lane (the workgroup's kMergeDims dims)
     static_assert(kMergeDims == 64 * PL, "merge: one lane per dim group");
@@ -641,19 +658,18 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
     __shared__ float s_m[MW], s_l[MW];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int h = blockIdx.x, ri = blockIdx.y, d0 = kMergeDims * int(blockIdx.z);
-    if (p.step) {
+    if (step) {
         // device-position step refused by the split kernel: no partials to merge
-        if (step_load(p.step + kStepError)) return;
+        if (step_load(step + kStepError)) return;
         // every split workgroup has read the position (they ran before this
         // launch): advance it for the next step, without waiting for the result
         if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0)
-            __hip_atomic_fetch_add(p.step + kStepPos, p.S, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(step + kStepPos, S, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const int rows = p.G * p.S;
-    const int ns = p.n_splits;  // <= kMaxSplits
-    const float2* ml = reinterpret_cast<const float2*>(p.partial + int64_t(p.Hkv) * ns * rows * D) +
-                       int64_t(h) * ns * rows + ri;
-    const float* po = p.partial + (int64_t(h) * ns * rows + ri) * D + d0 + PL * lane;
+    const int rows = G * S;
+    const int ns = n_splits;  // <= kMaxSplits
+    const float2* ml = reinterpret_cast<const float2*>(partial + ml_off) + int64_t(h) * ns * rows + ri;
+    const float* po = partial + (int64_t(h) * ns * rows + ri) * D + d0 + PL * lane;
     const int64_t sstride = int64_t(rows) * D;  // floats between splits
     static_assert(PL == 1, "merge: one dim per lane");
     auto load_o = [&](int s2, float (&o)[PL]) { o[0] = po[s2 * sstride]; };
@@ -715,8 +731,7 @@ __global__ __launch_bounds__(MW * 64) void paged_decode_merge_kernel(AttnParams 
             for (int e = 0; e < PL; ++e) O[e] += s_o[w2][PL * lane + e] * f;
         }
         const float inv = 1.0f / L;
-        uint16_t* orow = p.out + int64_t(h * p.G + ri % p.G) * p.o_head_stride + int64_t(ri / p.G) * p.o_tok_stride +
-                         d0 + PL * lane;
+        uint16_t* orow = out + int64_t(h * G + ri % G) * o_head_stride + int64_t(ri / G) * o_tok_stride + d0 + PL * lane;
         *orow = uint16_t(Elem<F16>::out(O[0] * inv));
     }
 }
@@ -802,16 +817,17 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
 
 template <int D, bool kStep, bool F16>
 void launch_split(const AttnParams& p, hipStream_t stream) {
-    bool wide = false;
+    auto* k = paged_decode_kernel<D, kWaves, kStep, F16>;
+    int w = kWaves;
     if constexpr (D == 128) {
-        wide = p.pages_per_split <= kWideMaxPps;
-        if (wide)
-            hipLaunchKernelGGL((paged_decode_kernel<D, kWideWaves, kStep, F16>), dim3(p.Hkv, p.n_splits),
-                               dim3(kWideWaves * 64), 0, stream, p);
+        if (p.pages_per_split <= kWideMaxPps) {
+            k = paged_decode_kernel<D, kWideWaves, kStep, F16>;
+            w = kWideWaves;
+        }
     }
-    if (!wide)
-        hipLaunchKernelGGL((paged_decode_kernel<D, kWaves, kStep, F16>), dim3(p.Hkv, p.n_splits), dim3(kWaves * 64),
-                           0, stream, p);
+    hipLaunchKernelGGL(k, dim3(p.Hkv, p.n_splits), dim3(w * 64), 0, stream, p.k_ids, p.v_ids, p.q,
+                       int32_t(p.q_head_stride), int32_t(p.q_tok_stride), p.G, p.S, p.pages_per_split, p.n_pages,
+                       p.upd.first, p.upd.count, p);
 }
 
 template <int D, bool F16>
@@ -823,10 +839,11 @@ int launch_decode_d(const AttnParams& p, hipStream_t stream) {
     GENLLM_LAUNCH_CHECK("paged_decode_kernel");
     if (p.n_splits > 1 && !p.counters) {
         const dim3 grid(p.Hkv, p.G * p.S, D / kMergeDims);
-        if (p.n_splits > 4 * kMergeU)
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 8, F16>), grid, dim3(8 * 64), 0, stream, p);
-        else
-            hipLaunchKernelGGL((paged_decode_merge_kernel<D, 4, F16>), grid, dim3(4 * 64), 0, stream, p);
+        const int32_t ml_off = p.Hkv * p.n_splits * p.G * p.S * D;  // < 2^31: the plan's workspace is far smaller
+        auto* mk = p.n_splits > 4 * kMergeU ? paged_decode_merge_kernel<D, 8, F16> : paged_decode_merge_kernel<D, 4, F16>;
+        const int mw = p.n_splits > 4 * kMergeU ? 8 : 4;
+        hipLaunchKernelGGL(mk, grid, dim3(mw * 64), 0, stream, static_cast<const float*>(p.partial), p.out,
+                           p.o_head_stride, p.o_tok_stride, p.n_splits, p.G, p.S, ml_off, p.step);
         GENLLM_LAUNCH_CHECK("paged_decode_merge_kernel");
     }
     return GENLLM_OK;
@@ -837,6 +854,8 @@ int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (p.n_pages <= 0) return GENLLM_OK;
     if (p.n_splits > kMaxSplits || p.pages_per_split <= 0 || p.G * p.S > kRows)
         return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
+    if (p.q_head_stride > INT32_MAX || p.q_tok_stride > INT32_MAX || p.q_head_stride < 0 || p.q_tok_stride < 0)
+        return fail(GENLLM_ERR_INVALID, "paged decode: q strides must be below 2^31 elements");
     if (p.f16) return head_dim == 128 ? launch_decode_d<128, true>(p, stream) : launch_decode_d<256, true>(p, stream);
     return head_dim == 128 ? launch_decode_d<128, false>(p, stream) : launch_decode_d<256, false>(p, stream);
 }
