@@ -166,3 +166,49 @@ def test_fill_normal_f16_matches_host_formula():
     ulp = np.maximum(np.abs(want), 2.0 ** -14) * 2.0 ** -10
     assert np.all(np.abs(got - want) <= ulp), np.max(np.abs(got - want) / ulp)
     assert abs(want.mean()) < 0.02 and abs(want.std() - 1) < 0.02
+
+
+@pytest.mark.parametrize("P,steps,merge", [(40, 12, "kernel"), (200, 6, "fused")])
+def test_f16_device_position_step(orc, request, P, steps, merge):
+    """fp16 layers through the device-position decode step: the step staged
+    (genllm_kv_stage_decode), genllm_paged_attention_step captured once into a
+    HIP graph and replayed token after token across a page boundary (and with
+    the single-launch merge), each replay against the oracle's fp16 path at the
+    host position, pools bit-exact; after genllm_kv_sync_decode the host page
+    table and num_cached equal the oracle's."""
+    if merge != "kernel":
+        paged.decode_tuning(0, merge)
+        request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
+    Hq, Hkv, D = 32, 8, 128
+    G, pool = Hq // Hkv, (P + steps + 15) // 16 + 3
+    mgr, ref = make(orc, Hkv, D, pool, 0x5EED0500 + P, orc.F16)
+    step(orc, mgr, ref, Hq, Hkv, P, D, 12000 + P, f"f16 prompt {P}")
+    dev = dict(dtype=torch.float16, device="cuda")
+    q_in, out = torch.zeros((1, Hq, 1, D), **dev), torch.zeros((1, Hq, 1, D), **dev)
+    k_in, v_in = torch.zeros((1, Hkv, 1, D), **dev), torch.zeros((1, Hkv, 1, D), **dev)
+    mgr.stage_decode(0, steps)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        paged.paged_attention_step(mgr, 0, q_in, k_in, v_in, out, G, scale_for(D))
+    for i in range(steps):
+        print(f"f16 step replay {i}: position {P + i} ({merge} merge)", flush=True)
+        q = synth.normal_f16(13000 + 10 * i, (1, Hq, 1, D))
+        k = synth.normal_f16(13001 + 10 * i, (1, Hkv, 1, D))
+        v = synth.normal_f16(13002 + 10 * i, (1, Hkv, 1, D))
+        q_in.copy_(paged.to_device_f16(q))
+        k_in.copy_(paged.to_device_f16(k))
+        v_in.copy_(paged.to_device_f16(v))
+        out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        want, rc = ref.paged_attention(0, q, k, v, G, scale_for(D), True, dtype=orc.F16)
+        assert rc == 0
+        assert_attn_close_f16(paged.to_host_bits(out), want, f"f16 step replay {i}")
+        check_pools(mgr, ref, f"f16 step replay {i}")
+    assert mgr.sync_decode(0) == P + steps
+    kt, vt = mgr.page_table(0)
+    rk, rv = ref.page_table(0)
+    assert np.array_equal(kt, rk) and np.array_equal(vt, rv)
+    assert mgr.get_layer(0).num_cached == ref.num_cached(0) == P + steps
+    mgr.close()
