@@ -129,7 +129,7 @@ def probe_lib():
         L = C.CDLL(os.path.join(ROOT, "genllm_amd", "libgenllm_probe.so"))
         P, i32 = C.c_void_p, C.c_int32
         L.genllm_probe_stream_read.argtypes = [P, C.c_size_t, P, P]
-        L.genllm_probe_decode_read.argtypes = [P, P, P, P, i32, i32, i32, i32, P, P]
+        L.genllm_probe_decode_read.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, P, P]
         L.genllm_probe_append_copy.argtypes = [P, P, P, P, P, P, i32, i32, i32, P]
         _probe = L
     return _probe
@@ -141,10 +141,15 @@ def _probe_call(name, *args):
         raise RuntimeError(f"{name} failed ({rc})")
 
 
-def decode_pps(torch, n_pages, Hkv):
-    """The decode kernel's default split size (about one workgroup per CU)."""
+def decode_pps(torch, n_pages, Hkv, D=128):
+    """The decode kernel's default plan: pages per split (about one workgroup
+    per CU) and kv heads per workgroup (4 once a one-head plan reaches 48
+    pages per split, for head_dim 128 and kv heads in groups of 4)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    return max(2, -(-n_pages * Hkv // cus), -(-n_pages // 256))
+    pps, heads = max(2, -(-n_pages * Hkv // cus)), 1
+    if D == 128 and Hkv % 4 == 0 and pps >= 48:
+        pps, heads = max(2, -(-n_pages * (Hkv // 4) // cus)), 4
+    return max(pps, -(-n_pages // 256)), heads
 
 
 def floor_entry(probe_us, nbytes, kernel_us, what):
@@ -288,17 +293,17 @@ def headline(args, np, torch, paged, synth, call):
     # read floors: the split kernel's exact page loads without the math (same
     # plan, same rotating layers), and a contiguous stream of the same bytes
     n_pages = (n_keys + PAGE - 1) // PAGE
-    pps = decode_pps(torch, n_pages, HKV3)
+    pps, hpw = decode_pps(torch, n_pages, HKV3)
     infos = [mgr.get_layer(l) for l in range(L)]
     sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
     cs = torch.cuda.current_stream().cuda_stream
     pat_us = time_kernels(torch, lambda i: _probe_call(
         "genllm_probe_decode_read", infos[i % L].k_pool, infos[i % L].v_pool, infos[i % L].k_ids,
-        infos[i % L].v_ids, n_pages, HKV3, D3, pps, sink.data_ptr(), cs), n_k, warm=args.warmup)
+        infos[i % L].v_ids, n_pages, HKV3, D3, pps, hpw, sink.data_ptr(), cs), n_k, warm=args.warmup)
     str_us = stream_floor(torch, kbytes, 16)
     floors = {"decode_config3_pattern": floor_entry(pat_us, kbytes, k_mean,
-                                                    f"the split kernel's page loads, {pps} pages per split, no math, "
-                                                    "no merge"),
+                                                    f"the split kernel's page loads, {pps} pages per split, "
+                                                    f"{hpw} kv head(s) per workgroup, no math, no merge"),
               "decode_config3_stream": floor_entry(str_us, kbytes, k_mean, "contiguous stream of the same bytes")}
     res = {
         "value": round(total_bytes / (step_s * args.steps) / 1e9, 1),
@@ -628,7 +633,7 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
     avg_us = time_kernels(torch, all_layers, iters, warm=2)
     # read floors: the split kernel's page loads of all 36 layers without the
     # math, and a contiguous stream of one layer's bytes
-    pps = decode_pps(torch, n_pages, Hkv)
+    pps, hpw = decode_pps(torch, n_pages, Hkv, D)
     sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
     cs = torch.cuda.current_stream().cuda_stream
 
@@ -636,14 +641,14 @@ def longctx_cfg5(np, torch, paged, synth, call, iters=10):
         for l in range(layers):
             inf = infos[l]
             _probe_call("genllm_probe_decode_read", inf.k_pool, inf.v_pool, inf.k_ids, inf.v_ids, n_pages, Hkv, D, pps,
-                        sink.data_ptr(), cs)
+                        hpw, sink.data_ptr(), cs)
 
     pat_us = time_kernels(torch, all_probes, iters, warm=2) / layers
     layer_bytes = decode_kernel_bytes(N)
     str_us = stream_floor(torch, layer_bytes, 8, iters=20)
     floors = {"decode_config5_pattern": floor_entry(pat_us, layer_bytes, avg_us / layers,
                                                     f"the split kernel's page loads per layer, {pps} pages per split, "
-                                                    "no math, no merge"),
+                                                    f"{hpw} kv head(s) per workgroup, no math, no merge"),
               "decode_config5_stream": floor_entry(str_us, layer_bytes, avg_us / layers,
                                                    "contiguous stream of one layer's bytes")}
     # the same 36-layer sequence captured once into a HIP graph and replayed

@@ -97,7 +97,7 @@ SIGNATURES = {
     "genllm_rope_cache": (_int, [_P, _f, _i32, _i32, _i32]),
     "genllm_kv_scatter": (_int, [_P, _i64, _i64, _P, _i64, _i64, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _P]),
     "genllm_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
-    "genllm_decode_tuning": (_int, [_i32, _i32]),
+    "genllm_decode_tuning": (_int, [_i32, _i32, _i32]),
     "genllm_paged_decode": (_int, [_P, _i64, _i64, _P, _i64, _i64, _P, _P, _P, _P, _i32, _i32, _i32, _i32, _i32,
                                    _i32, _f, _i32, _P, _sz, _P]),
     "genllm_paged_decode_noalloc": (_int, [_P, _i64, _i64, _P, _i64, _i64, _P, _P, _P, _P, _i32, _i32, _i32, _i32,

@@ -78,7 +78,8 @@ struct AttnParams {
     int64_t kv_head_stride = 0;
     // split-K decode: per-split partials [unit][split][row][D] then {m, l} per (unit, split, row)
     float* partial = nullptr;
-    int32_t pages_per_split = 0, n_splits = 1, n_chunks = 1;
+    int32_t pages_per_split = 0, n_splits = 1;
+    int32_t heads_per_wg = 1;  // kv heads per split workgroup (1, or 4 for long page ranges)
     // Single-launch merge: per-kv-head arrival counters (zero between
     // launches); the last split workgroup of a head to arrive merges them.
     // nullptr = merge in a second kernel.
@@ -118,7 +119,7 @@ constexpr int kStepPos = 0, kStepLimit = 1, kStepArrivals = 2, kStepError = 3, k
 size_t decode_workspace_bytes(int Hq, int Hkv, int S, int D, int n_pages);
 // Decode merge forms (genllm_decode_tuning)
 constexpr int kDecodeMergeKernel = 0, kDecodeMergeFused = 1;
-int set_decode_tuning(int pages_per_split, int merge);
+int set_decode_tuning(int pages_per_split, int merge, int heads_per_wg);
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws);
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream);
 int launch_paged_prefill(const AttnParams& p, int head_dim, hipStream_t stream);

@@ -1082,8 +1082,8 @@ extern "C" int genllm_kv_scatter(const void* k, int64_t k_tok_stride, int64_t k_
     return launch_kv_append(ap, head_dim, as_stream(stream));
 }
 
-extern "C" int genllm_decode_tuning(int32_t pages_per_split, int32_t merge) {
-    return set_decode_tuning(pages_per_split, merge);
+extern "C" int genllm_decode_tuning(int32_t pages_per_split, int32_t merge, int32_t heads_per_workgroup) {
+    return set_decode_tuning(pages_per_split, merge, heads_per_workgroup);
 }
 
 extern "C" size_t genllm_paged_decode_workspace_bytes(int32_t n_q_heads, int32_t n_kv_heads, int32_t seq_len,

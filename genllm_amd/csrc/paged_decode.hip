@@ -5,8 +5,9 @@
 //   out[q] = sum_t softmax_t(scale * q.k_t) v_t over keys t <= q_abs (causal)
 // with kv head h = q head / groups (:158) and q_abs = n_cached - S + s (:164).
 //
-// Split kernel: grid (Hkv, splits), W = 4 or 8 waves.  A workgroup owns one
-// kv head and a contiguous range of pages; its waves take pages round-robin.
+// Split kernel: grid (Hkv / HPW, splits), W = 4 or 8 waves.  A workgroup owns
+// HPW kv heads (1, or 4 for long page ranges) and a contiguous range of
+// pages; the W / HPW waves of each head take its pages round-robin.
 // The kv head is the fastest grid index: the dispatcher deals workgroups to the
 // 8 XCDs round-robin, so with 8 kv heads every split of head h (and, with the
 // same order in the merge grid, that head's merge) runs on XCD h.  8 waves
@@ -59,6 +60,16 @@ constexpr int kWideWaves = 8;   // waves of a split workgroup over short ranges 
 // pages: 29.5 against 31.0 us per layer with 4 waves, and 30.1 against 31.2
 // for the captured decode step, whose plan covers 65)
 constexpr int kWideMaxPps = 128;
+// Long page ranges: 4 kv heads per 8-wave workgroup (2 waves per head), so
+// that a workgroup reads 1 KB of every token row of its pages instead of one
+// head's 256 bytes at a 2 KB stride, for 4x the splits.  Used when a one-head
+// plan would give kMultiHeadMinPps pages per split or more (config 5's 64;
+// config 3's 16 keeps one head).  Measured at config 5 (A/B on one box, two
+// passes): 27.6-27.8 against 28.8-28.9 us per layer eager, 29.1 against 30.2
+// as a replayed graph; 2 heads per workgroup 27.8-28.0 (graph 28.6), 8 heads
+// 29.7, 4 heads with two pages in flight per wave 28.2.
+constexpr int kMultiHead = 4;
+constexpr int kMultiHeadMinPps = 48;
 constexpr int kMergeU = 16;     // splits in flight per merge lane
 constexpr size_t kSplitLeadArgBytes = 56;  // the split kernel's scalar arguments ahead of the parameter block
 constexpr int kMergeDims = 64;  // dims per merge workgroup
@@ -229,7 +240,7 @@ __device__ __forceinline__ int step_load(const int32_t* at) {
 // by this call, q) come first as scalars (14 dwords), ahead of the parameter
 // block, so that they can be preloaded into SGPRs at wave launch: the page-id
 // and q loads then leave without an argument read before them.
-template <int D, int W, bool kStep, bool F16>
+template <int D, int W, bool kStep, bool F16, int HPW>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_ids, const int32_t* v_ids,
                                                               const uint16_t* q, int32_t q_head_stride,
                                                               int32_t q_tok_stride, int32_t G, int32_t S,
@@ -250,7 +261,12 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
     // branches below are then wave-uniform to the compiler as well
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n16 = lane & 15, g = lane >> 4;
-    const int h = blockIdx.x, sp = blockIdx.y;
+    // HPW kv heads per workgroup: waves [WP lh, WP lh + WP) serve head
+    // blockIdx.x HPW + lh and take its pages round-robin
+    constexpr int WP = W / HPW;
+    static_assert(W % HPW == 0, "decode kernel: whole waves per kv head");
+    const int lh = HPW == 1 ? 0 : wv / WP, wi = HPW == 1 ? wv : wv - lh * WP;
+    const int h = int(blockIdx.x) * HPW + lh, sp = blockIdx.y;
     const int rows_total = G * S;  // <= 16
 
     // q rows and the block-table entries of the wave's planned page range are
@@ -272,9 +288,9 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
     }
     const int begin = sp * pages_per_split;
     const int end_plan = min(begin + pages_per_split, n_pages_arg);
-    const int np_plan = end_plan - begin - wv > 0 ? (end_plan - begin - wv + W - 1) / W : 0;
+    const int np_plan = end_plan - begin - wi > 0 ? (end_plan - begin - wi + WP - 1) / WP : 0;
     // fused append: page ids opened by this call come from the launch arguments
-    if (sp == 0 && h == 0 && threadIdx.x < upd_count) {
+    if (sp == 0 && blockIdx.x == 0 && threadIdx.x < upd_count) {
         p.k_ids_w[upd_first + threadIdx.x] = p.upd.k[threadIdx.x];
         p.v_ids_w[upd_first + threadIdx.x] = p.upd.v[threadIdx.x];
     }
@@ -289,7 +305,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
         kid = vid = 0;
         const int jj = 64 * b + lane;
         if (jj < np_plan) {
-            const int pg = begin + wv + W * jj;
+            const int pg = begin + wi + WP * jj;
             const int rel = pg - upd_first;
             if (rel >= 0 && rel < upd_count) {
                 kid = p.upd.k[rel];
@@ -327,7 +343,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
 
     const int qabs = p.causal ? n_cached - p.S + r / p.G : n_cached - 1;
     const int end = min(begin + pages_per_split, n_pages);
-    const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;  // <= np_plan
+    const int np = end - begin - wi > 0 ? (end - begin - wi + WP - 1) / WP : 0;  // <= np_plan
     // Element offsets inside a page (< 2^31): lane's K operand chunk (token
     // n16, dims 8g + 32c) and V row chunk (token 4g + i, dims 8 n16).  Page
     // bases are wave-uniform, so a load is a scalar base plus this offset.
@@ -342,7 +358,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
     // tokens.  Only they take the per-token conditions below.
     const int lo_tok = min(p.causal ? n_cached - p.S + 1 : n_cached, new_from);
     const int special_from = lo_tok / kPage;
-    auto page_of = [&](int j) { return begin + wv + W * j; };
+    auto page_of = [&](int j) { return begin + wi + WP * j; };
 
     // Token t >= new_from is this call's append: read it from k_new / v_new.
     auto load_page = [&](int j, PageRegs<D>& pr, bool special) {
@@ -561,18 +577,20 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
     }
     __syncthreads();
 
-    // workgroup merge: wave -> rows ri, ri+4, ...; lane -> dims d2, d2+1 of
-    // each 128-dim half
-    for (int ri = wv; ri < rows_total; ri += W) {
+    // workgroup merge of each head's waves: wave -> (head, row) pairs wv,
+    // wv + W, ...; lane -> dims d2, d2+1 of each 128-dim half
+    for (int idx = wv; idx < HPW * rows_total; idx += W) {
+        const int mh = HPW == 1 ? 0 : idx / rows_total, ri = idx - mh * rows_total;
+        const int h = int(blockIdx.x) * HPW + mh, w0 = WP * mh;  // the pair's kv head, its first wave
         float M = -INFINITY;
 #pragma unroll
-        for (int w2 = 0; w2 < W; ++w2) M = fmaxf(M, lds_m[w2][ri]);
+        for (int w2 = w0; w2 < w0 + WP; ++w2) M = fmaxf(M, lds_m[w2][ri]);
         float L = 0.0f, O0[VH], O1[VH];
 #pragma unroll
         for (int hh = 0; hh < VH; ++hh) O0[hh] = O1[hh] = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int w2 = 0; w2 < W; ++w2) {
+            for (int w2 = w0; w2 < w0 + WP; ++w2) {
                 const float e = exp2_fast(lds_m[w2][ri] - M);
                 L += lds_l[w2][ri] * e;
 #pragma unroll
@@ -625,7 +643,9 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
             }
         }
     }
-    if (p.counters && p.n_splits > 1) merge_last_arrival<D, W, F16>(p, h, lds_m, lds_l, lds_o);
+    if constexpr (HPW == 1) {
+        if (p.counters && p.n_splits > 1) merge_last_arrival<D, W, F16>(p, h, lds_m, lds_l, lds_o);
+    }
 }
 
 // Merge of the splits: one workgroup of MW waves per (kv head, row, 64-dim
@@ -760,8 +780,10 @@ struct DecodeSettings {
     std::atomic<int> pps{0};          // > 0: forced pages per split
     std::atomic<double> wg_per_cu{1.0};
     std::atomic<int> merge{kDecodeMergeKernel};
+    std::atomic<int> heads{0};        // kv heads per split workgroup: 0 automatic, 1 or kMultiHead forced
     DecodeSettings() {
         if (const char* e = getenv("GENLLM_DECODE_PPS")) pps = atoi(e);
+        if (const char* e = getenv("GENLLM_DECODE_HEADS")) heads = atoi(e);
         if (const char* e = getenv("GENLLM_DECODE_WG_PER_CU")) wg_per_cu = atof(e);
         if (const char* e = getenv("GENLLM_DECODE_MERGE")) {
             const std::string m(e);
@@ -775,26 +797,42 @@ DecodeSettings& decode_settings() {
 }
 }  // namespace
 
-int set_decode_tuning(int pages_per_split, int merge) {
+int set_decode_tuning(int pages_per_split, int merge, int heads_per_wg) {
     if (merge != kDecodeMergeKernel && merge != kDecodeMergeFused)
         return fail(GENLLM_ERR_INVALID, "decode tuning: merge must be 0 (merge kernel) or 1 (fused)");
+    if (heads_per_wg != 0 && heads_per_wg != 1 && heads_per_wg != kMultiHead)
+        return fail(GENLLM_ERR_INVALID, "decode tuning: heads per workgroup must be 0 (automatic), 1 or 4");
     decode_settings().pps = std::max(pages_per_split, 0);
     decode_settings().merge = merge;
+    decode_settings().heads = heads_per_wg;
     return GENLLM_OK;
 }
 
 // Pages per split: about wg_per_cu (default 1) workgroups per CU over all kv
 // heads, at most 256 splits (a forced value, genllm_decode_tuning, wins).
+// Heads per workgroup: kMultiHead where the one-head plan reaches
+// kMultiHeadMinPps pages per split (or where forced), for head_dim 128, kv
+// heads in groups of 4 and the merge kernel; else 1.
 int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
     if (p.G * p.S > kRows) return fail(GENLLM_ERR_INVALID, "paged decode: seq_len * groups must be <= 16");
     DecodeSettings& cfg = decode_settings();
-    p.n_chunks = 1;
+    p.heads_per_wg = 1;
     int pps = cfg.pps.load(std::memory_order_relaxed);
+    const int heads = cfg.heads.load(std::memory_order_relaxed);
     const int cus = device_cu_count();
+    const bool multi_ok =
+        D == 128 && p.Hkv % kMultiHead == 0 && cfg.merge.load(std::memory_order_relaxed) == kDecodeMergeKernel;
     if (pps <= 0) {
         const int64_t target = std::max<int64_t>(1, int64_t(cfg.wg_per_cu.load(std::memory_order_relaxed) * cus));
         pps = int((int64_t(p.n_pages) * p.Hkv + target - 1) / target);
         if (pps < 2) pps = 2;
+        // long ranges: kMultiHead kv heads per workgroup, the same workgroup count
+        if (multi_ok && (heads == kMultiHead || (heads == 0 && pps >= kMultiHeadMinPps))) {
+            p.heads_per_wg = kMultiHead;
+            pps = std::max(2, int((int64_t(p.n_pages) * (p.Hkv / kMultiHead) + target - 1) / target));
+        }
+    } else if (multi_ok && heads == kMultiHead) {
+        p.heads_per_wg = kMultiHead;
     }
     pps = std::max(pps, (p.n_pages + kMaxSplits - 1) / kMaxSplits);
     p.pages_per_split = pps;
@@ -817,15 +855,19 @@ int decode_plan(AttnParams& p, int D, size_t ws_bytes, void* ws) {
 
 template <int D, bool kStep, bool F16>
 void launch_split(const AttnParams& p, hipStream_t stream) {
-    auto* k = paged_decode_kernel<D, kWaves, kStep, F16>;
-    int w = kWaves;
+    auto* k = paged_decode_kernel<D, kWaves, kStep, F16, 1>;
+    int w = kWaves, hpw = 1;
     if constexpr (D == 128) {
-        if (p.pages_per_split <= kWideMaxPps) {
-            k = paged_decode_kernel<D, kWideWaves, kStep, F16>;
+        if (p.heads_per_wg == kMultiHead) {
+            k = paged_decode_kernel<D, kWideWaves, kStep, F16, kMultiHead>;
+            w = kWideWaves;
+            hpw = kMultiHead;
+        } else if (p.pages_per_split <= kWideMaxPps) {
+            k = paged_decode_kernel<D, kWideWaves, kStep, F16, 1>;
             w = kWideWaves;
         }
     }
-    hipLaunchKernelGGL(k, dim3(p.Hkv, p.n_splits), dim3(w * 64), 0, stream, p.k_ids, p.v_ids, p.q,
+    hipLaunchKernelGGL(k, dim3(p.Hkv / hpw, p.n_splits), dim3(w * 64), 0, stream, p.k_ids, p.v_ids, p.q,
                        int32_t(p.q_head_stride), int32_t(p.q_tok_stride), p.G, p.S, p.pages_per_split, p.n_pages,
                        p.upd.first, p.upd.count, p);
 }
@@ -852,7 +894,8 @@ int launch_decode_d(const AttnParams& p, hipStream_t stream) {
 int launch_paged_decode(const AttnParams& p, int head_dim, hipStream_t stream) {
     if (head_dim != 128 && head_dim != 256) return fail(GENLLM_ERR_UNSUPPORTED, "paged decode: head_dim must be 128 or 256");
     if (p.n_pages <= 0) return GENLLM_OK;
-    if (p.n_splits > kMaxSplits || p.pages_per_split <= 0 || p.G * p.S > kRows)
+    if (p.n_splits > kMaxSplits || p.pages_per_split <= 0 || p.G * p.S > kRows ||
+        (p.heads_per_wg != 1 && (p.heads_per_wg != kMultiHead || head_dim != 128 || p.Hkv % kMultiHead || p.counters)))
         return fail(GENLLM_ERR_INVALID, "paged decode: split plan out of range");
     if (p.q_head_stride > INT32_MAX || p.q_tok_stride > INT32_MAX || p.q_head_stride < 0 || p.q_tok_stride < 0)
         return fail(GENLLM_ERR_INVALID, "paged decode: q strides must be below 2^31 elements");

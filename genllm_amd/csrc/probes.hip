@@ -6,9 +6,10 @@
 //   * genllm_probe_stream_read: a contiguous stream of `bytes` (one 16-byte
 //     nontemporal load per thread) -- the best case for that many bytes;
 //   * genllm_probe_decode_read: the split decode kernel's page loads (grid
-//     (Hkv, splits), 8 waves up to 128 pages per split else 4, pages dealt to
-//     the waves round-robin, one page in flight per wave, K operand chunks and
-//     V rows with 16-byte nt buffer loads), folded with XOR instead of the
+//     (Hkv / heads per workgroup, splits), 8 waves up to 128 pages per split
+//     or with 4 heads per workgroup, else 4, each head's pages dealt to its
+//     waves round-robin, one page in flight per wave, K operand chunks and V
+//     rows with 16-byte nt buffer loads), folded with XOR instead of the
 //     attention math and the split merge;
 //   * genllm_probe_append_copy: the fused append's data movement (one wave per
 //     8 rows of one token: K rows as 8-byte loads and, after a lane-pair swap,
@@ -38,7 +39,7 @@ __global__ __launch_bounds__(256) void probe_stream_kernel(const u32x4* p, int64
     if (acc == 0x9E3779B9u) sink[blockIdx.x & 0xFFFF] = acc;
 }
 
-template <int D, int W>
+template <int D, int W, int HPW>
 __global__ __launch_bounds__(W * 64) void probe_decode_kernel(const uint16_t* k_pool, const uint16_t* v_pool,
                                                               const int32_t* k_ids, const int32_t* v_ids, int n_pages,
                                                               int pps, int64_t page_elems, int64_t kv_row,
@@ -46,11 +47,12 @@ __global__ __launch_bounds__(W * 64) void probe_decode_kernel(const uint16_t* k_
     constexpr int KS = D / 32, VH = D / 128;
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n16 = lane & 15, g = lane >> 4;
-    const int h = blockIdx.x, sp = blockIdx.y;
+    constexpr int WP = W / HPW;  // waves per kv head
+    const int h = int(blockIdx.x) * HPW + wv / WP, wi = wv % WP, sp = blockIdx.y;
     const int begin = sp * pps, end = min(begin + pps, n_pages);
-    const int np = end - begin - wv > 0 ? (end - begin - wv + W - 1) / W : 0;  // <= 64 (checked by the host)
-    const int kid = lane < np ? k_ids[begin + wv + W * lane] : 0;
-    const int vid = lane < np ? v_ids[begin + wv + W * lane] : 0;
+    const int np = end - begin - wi > 0 ? (end - begin - wi + WP - 1) / WP : 0;  // <= 64 (checked by the host)
+    const int kid = lane < np ? k_ids[begin + wi + WP * lane] : 0;
+    const int vid = lane < np ? v_ids[begin + wi + WP * lane] : 0;
     const int kcol_b = int(2 * (h * D + n16 * kv_row + 8 * g)), vcol_b = int(2 * (h * D + 4 * g * kv_row + 8 * n16));
     const int row_b = int(2 * kv_row), page_b = int(2 * page_elems);
     uint32_t acc = 0;
@@ -147,24 +149,30 @@ extern "C" int genllm_probe_stream_read(const void* p, size_t bytes, void* sink,
 }
 
 // The decode's page loads for n_pages pages of n_kv_heads heads (page layout
-// [16][Hkv][D]) in splits of pages_per_split pages.
+// [16][Hkv][D]) in splits of pages_per_split pages, heads_per_wg (1 or 4) kv
+// heads per workgroup.
 extern "C" int genllm_probe_decode_read(const void* k_pool, const void* v_pool, const int32_t* k_ids,
                                         const int32_t* v_ids, int32_t n_pages, int32_t n_kv_heads, int32_t head_dim,
-                                        int32_t pages_per_split, void* sink, void* stream) {
+                                        int32_t pages_per_split, int32_t heads_per_wg, void* sink, void* stream) {
     if (!k_pool || !v_pool || !k_ids || !v_ids || !sink || n_pages <= 0 || n_kv_heads <= 0 || pages_per_split <= 0)
         return GENLLM_ERR_INVALID;
     if (head_dim != 128 || pages_per_split > 64 * 4) return GENLLM_ERR_UNSUPPORTED;
+    if (heads_per_wg != 1 && (heads_per_wg != 4 || n_kv_heads % 4 || pages_per_split > 64 * 2))
+        return GENLLM_ERR_UNSUPPORTED;
     const int splits = (n_pages + pages_per_split - 1) / pages_per_split;
     const int64_t kv_row = int64_t(n_kv_heads) * head_dim, page_elems = kPage * kv_row;
     const auto s = static_cast<hipStream_t>(stream);
     const auto* kp = static_cast<const uint16_t*>(k_pool);
     const auto* vp = static_cast<const uint16_t*>(v_pool);
     auto* o = static_cast<uint32_t*>(sink);
-    if (pages_per_split <= 128 && pages_per_split <= 64 * 8)
-        hipLaunchKernelGGL((probe_decode_kernel<128, 8>), dim3(n_kv_heads, splits), dim3(512), 0, s, kp, vp, k_ids,
+    if (heads_per_wg == 4)
+        hipLaunchKernelGGL((probe_decode_kernel<128, 8, 4>), dim3(n_kv_heads / 4, splits), dim3(512), 0, s, kp, vp,
+                           k_ids, v_ids, n_pages, pages_per_split, page_elems, kv_row, o);
+    else if (pages_per_split <= 128)
+        hipLaunchKernelGGL((probe_decode_kernel<128, 8, 1>), dim3(n_kv_heads, splits), dim3(512), 0, s, kp, vp, k_ids,
                            v_ids, n_pages, pages_per_split, page_elems, kv_row, o);
     else
-        hipLaunchKernelGGL((probe_decode_kernel<128, 4>), dim3(n_kv_heads, splits), dim3(256), 0, s, kp, vp, k_ids,
+        hipLaunchKernelGGL((probe_decode_kernel<128, 4, 1>), dim3(n_kv_heads, splits), dim3(256), 0, s, kp, vp, k_ids,
                            v_ids, n_pages, pages_per_split, page_elems, kv_row, o);
     return hipGetLastError() == hipSuccess ? GENLLM_OK : GENLLM_ERR_HIP;
 }

@@ -332,20 +332,21 @@ def paged_decode(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: i
 DECODE_MERGE = {"kernel": 0, "fused": 1}
 
 
-def decode_tuning(pages_per_split: int = 0, merge: str = "kernel"):
-    """genllm_decode_tuning: process-wide decode split size (0 = automatic)
-    and merge form ("kernel" or "fused") for later decode calls."""
-    call("genllm_decode_tuning", int(pages_per_split), DECODE_MERGE[merge])
+def decode_tuning(pages_per_split: int = 0, merge: str = "kernel", heads: int = 0):
+    """genllm_decode_tuning: process-wide decode split size (0 = automatic),
+    merge form ("kernel" or "fused") and kv heads per split workgroup (0 =
+    automatic, 1 or 4) for later decode calls."""
+    call("genllm_decode_tuning", int(pages_per_split), DECODE_MERGE[merge], int(heads))
 
 
 @contextlib.contextmanager
-def decode_tuned(pages_per_split: int = 0, merge: str = "kernel"):
+def decode_tuned(pages_per_split: int = 0, merge: str = "kernel", heads: int = 0):
     """decode_tuning for the duration of a with-block, then the defaults."""
-    decode_tuning(pages_per_split, merge)
+    decode_tuning(pages_per_split, merge, heads)
     try:
         yield
     finally:
-        decode_tuning(0, "kernel")
+        decode_tuning(0, "kernel", 0)
 
 
 def paged_decode_noalloc(q, out, k_pool, v_pool, k_ids, v_ids, n_pages: int, n_cached: int, n_kv_heads: int,

@@ -262,11 +262,14 @@ int genllm_paged_decode(const void *q, int64_t q_head_stride, int64_t q_tok_stri
  * device-position steps), process-wide, for later calls.  pages_per_split > 0
  * forces the split size (0: automatic, about one workgroup per CU).  merge:
  * 0 = a merge kernel after the split kernel (default), 1 = the last split
- * workgroup of each kv head to finish merges it in the same launch.  The
- * initial values come from GENLLM_DECODE_PPS and GENLLM_DECODE_MERGE
- * (kernel | fused), read once.  Returns GENLLM_ERR_INVALID for another merge
- * value. */
-int genllm_decode_tuning(int32_t pages_per_split, int32_t merge);
+ * workgroup of each kv head to finish merges it in the same launch.
+ * heads_per_workgroup: kv heads one split workgroup reads; 0 = automatic (4
+ * for long page ranges, else 1), 1, or 4 (taken where head_dim is 128, the kv
+ * heads come in groups of 4 and the merge runs in a kernel; else 1).  The
+ * initial values come from GENLLM_DECODE_PPS, GENLLM_DECODE_MERGE (kernel |
+ * fused) and GENLLM_DECODE_HEADS, read once.  Returns GENLLM_ERR_INVALID for
+ * another merge or heads value. */
+int genllm_decode_tuning(int32_t pages_per_split, int32_t merge, int32_t heads_per_workgroup);
 
 /* No counterpart in the reference: genllm_paged_decode for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

@@ -46,13 +46,13 @@ class Context:
         self.info = self.mgr.get_layer(0)
         self.n_ctx = n_ctx
 
-    def decode(self, q_bits, causal=True, pps=None, merge=None):
+    def decode(self, q_bits, causal=True, pps=None, merge=None, heads=0):
         Hq, S, D = q_bits.shape
         out = torch.zeros((Hq, S, D), dtype=torch.bfloat16, device="cuda")
         n_pages = (self.n_ctx + 15) // 16
         ws = torch.zeros(paged.decode_workspace_bytes(Hq, self.Hkv, S, D, n_pages), dtype=torch.uint8,
                          device="cuda")
-        with paged.decode_tuned(pps or 0, merge or "kernel"):
+        with paged.decode_tuned(pps or 0, merge or "kernel", heads):
             info = self.info
             paged.paged_decode(paged.to_device_bf16(q_bits), out, info.k_pool, info.v_pool, info.k_ids, info.v_ids,
                                n_pages, self.n_ctx, self.Hkv, scale_for(D), ws, causal=causal)
@@ -125,6 +125,48 @@ def test_decode_wave_forms(orc, pps):
     got2, _ = ctx.decode(q, pps=pps)
     assert np.array_equal(got, got2)
     ctx.close()
+
+
+@pytest.mark.parametrize("pps", [None, 1, 2, 7, 16, 64, 129])
+def test_decode_four_heads_per_workgroup(orc, pps):
+    """Split workgroups that read 4 kv heads of their pages (the plan for long
+    page ranges; forced here at every split size, 2 waves per head) against
+    the oracle over 4100 keys with a NaN/-inf tail past the cache end, twice
+    on one workspace (bit-identical)."""
+    ctx = Context(orc, 8, 128, 300, 4100, 191 + (pps or 0), nan_tail=True)
+    q = synth.normal_bf16(192 + (pps or 0), (32, 1, 128))
+    ref = ctx.oracle(q)
+    got, _ = ctx.decode(q, pps=pps, heads=4)
+    assert_attn_close(got, ref, f"4 heads pps{pps}")
+    got2, _ = ctx.decode(q, pps=pps, heads=4)
+    assert np.array_equal(got, got2)
+    one, _ = ctx.decode(q, pps=pps, heads=1)
+    assert_attn_close(got, one, f"4 heads against 1, pps{pps}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,causal,N", [(2, 32, 8, True, 3000), (4, 32, 8, True, 1000), (8, 16, 8, True, 777),
+                                               (2, 32, 8, False, 1000), (1, 16, 4, True, 2049), (16, 4, 4, True, 300)])
+def test_decode_four_heads_rows(orc, S, Hq, Hkv, causal, N):
+    """4 kv heads per split workgroup with several query rows per kv head (up
+    to 16: 64 (head, row) pairs merged by the workgroup's 8 waves), causal and
+    not, against the oracle."""
+    ctx = Context(orc, Hkv, 128, (N + 15) // 16 + 3, N, 700 + S + N, nan_tail=True)
+    q = synth.normal_bf16(701 + S, (Hq, S, 128))
+    got, _ = ctx.decode(q, causal=causal, heads=4)
+    assert_attn_close(got, ctx.oracle(q, causal), f"4 heads S{S} Hq{Hq} Hkv{Hkv} causal{causal}")
+    ctx.close()
+
+
+def test_decode_four_heads_fall_back(orc):
+    """Shapes the 4-head form does not serve (2 kv heads; head_dim 256; the
+    single-launch merge) run the 1-head form when 4 are asked for."""
+    for Hkv, D, merge in ((2, 128, "kernel"), (8, 256, "kernel"), (8, 128, "fused")):
+        ctx = Context(orc, Hkv, D, 80, 1200, 910 + Hkv + D, nan_tail=True)
+        q = synth.normal_bf16(911 + D, (4 * Hkv, 1, D))
+        got, _ = ctx.decode(q, merge=merge, heads=4)
+        assert_attn_close(got, ctx.oracle(q), f"fall back Hkv{Hkv} D{D} {merge}")
+        ctx.close()
 
 
 @pytest.mark.parametrize("S,Hq,causal", [(2, 32, True), (4, 32, True), (3, 16, True), (8, 16, True),

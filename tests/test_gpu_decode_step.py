@@ -254,13 +254,17 @@ def test_step_head_dim_256_across_8192(orc):
     (32, 8, 128, 1, 5, 128, None),      # one split: the last split workgroup advances the position
     (32, 8, 128, 1, 200, 128, "fused"),  # single-launch merge: no merge kernel either
     (8, 2, 256, 1, 90, 64, None),       # Qwen3.5: RoPE on the first 64 of 256 dims
+    (16, 8, 128, 2, 40, 128, "heads4"),  # split workgroups reading 4 kv heads each, steps crossing pages
 ])
 def test_step_variants(orc, request, Hq, Hkv, D, S, P, rope_dim, merge):
     """Device-position steps beyond the single-token default plan: the query
     chunk, the split plan, the merge form and the rotary width change, and
     every replay still matches the oracle run with host positions (RoPE'd q
     bit-exact, attention within tolerance, pools bit-exact)."""
-    if merge:
+    if merge == "heads4":
+        paged.decode_tuning(0, "kernel", 4)
+        request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
+    elif merge:
         paged.decode_tuning(0, merge)
         request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
     G, L, steps, max_seq = Hq // Hkv, 2, 8, 512

@@ -168,7 +168,7 @@ def test_fill_normal_f16_matches_host_formula():
     assert abs(want.mean()) < 0.02 and abs(want.std() - 1) < 0.02
 
 
-@pytest.mark.parametrize("P,steps,merge", [(40, 12, "kernel"), (200, 6, "fused")])
+@pytest.mark.parametrize("P,steps,merge", [(40, 12, "kernel"), (200, 6, "fused"), (40, 12, "heads4")])
 def test_f16_device_position_step(orc, request, P, steps, merge):
     """fp16 layers through the device-position decode step: the step staged
     (genllm_kv_stage_decode), genllm_paged_attention_step captured once into a
@@ -176,7 +176,10 @@ def test_f16_device_position_step(orc, request, P, steps, merge):
     the single-launch merge), each replay against the oracle's fp16 path at the
     host position, pools bit-exact; after genllm_kv_sync_decode the host page
     table and num_cached equal the oracle's."""
-    if merge != "kernel":
+    if merge == "heads4":  # split workgroups reading 4 kv heads each
+        paged.decode_tuning(0, "kernel", 4)
+        request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
+    elif merge != "kernel":
         paged.decode_tuning(0, merge)
         request.addfinalizer(lambda: paged.decode_tuning(0, "kernel"))
     Hq, Hkv, D = 32, 8, 128
