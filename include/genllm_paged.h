@@ -279,8 +279,10 @@ int genllm_decode_tuning(int32_t pages_per_split, int32_t merge, int32_t heads_p
  * ends.  The call allocates nothing; its first call on a device resolves that
  * device's scratch and clears its counters with a small kernel on `stream`.
  * A launch whose split plan needs more scratch (kv heads x splits x rows x
- * (head_dim + 2) x 4 bytes + 1 KiB; the Qwen3-4B decode at 8K or 32K keys
- * needs about 0.5 MiB) returns GENLLM_ERR_INVALID and launches nothing.
+ * (head_dim + 2) x 4 bytes + 1 KiB; the Qwen3-4B decode needs about 0.5
+ * MiB at 8K keys and 2.1 MiB from 32K keys on, where its plan takes 4 kv
+ * heads per split workgroup and 128 splits) returns GENLLM_ERR_INVALID and
+ * launches nothing.
  * Every call on a GPU shares that GPU's scratch: calls that overlap on one
  * GPU (different streams, threads) race; calls ordered on one stream do not. */
 #define GENLLM_NOALLOC_SCRATCH_BYTES (4u << 20)

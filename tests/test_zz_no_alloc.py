@@ -90,6 +90,23 @@ def test_noalloc_matches_workspace_entry_point(orc, merge, request):
     c2.close()
 
 
+def test_noalloc_long_context_four_heads(orc):
+    """At config 5's length (32,761 keys) the plan reads 4 kv heads per split
+    workgroup over 128 splits (2.1 MiB of partials, inside the scratch): the
+    allocation-free call matches the workspace call bit for bit, and the
+    oracle to the attention tolerance; then a shorter call (one-head plan)."""
+    c = Cache(orc, 8, 128, 2060, 32761, 0x5EED0905)
+    q1 = synth.normal_bf16(0x5EED0906, (32, 1, 128))
+    a = c.run(q1, 32761, noalloc=True)
+    b = c.run(q1, 32761, noalloc=False)
+    assert np.array_equal(a, b), "noalloc differs from the workspace entry point (32761 keys)"
+    assert_attn_close(a, c.oracle(q1), "noalloc 32761 keys")
+    a2 = c.run(q1, 8193, noalloc=True)
+    b2 = c.run(q1, 8193, noalloc=False)
+    assert np.array_equal(a2, b2), "noalloc differs from the workspace entry point (8193 keys after 32761)"
+    c.close()
+
+
 def test_noalloc_refuses_plans_beyond_its_scratch(orc, request):
     """16 rows per kv head over 8 kv heads at 8193 keys with 3 pages per
     split: 8 x 171 splits x 16 rows x 130 x 4 B = 11.4 MB of partials, more
