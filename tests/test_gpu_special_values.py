@@ -16,8 +16,11 @@ o, the kernels' masked scores are -inf before the exponent.  A NaN in V is
 different in the prefill kernel: the keys of a diagonal tile past a query's
 limit meet a zero probability in the P.V matrix product, and 0 x NaN is
 NaN, where the reference never visits those keys.  The queries so exposed
-are the at most 31 before the row in the same 32-query wave; for them the
-NaN dims may be NaN or match, and every other dim must match."""
+sit at most 46 positions before the row: a wave of 16 queries multiplies
+the whole 32-key half it processes, and it processes a half that starts
+before its last query, so the key can lie up to 15 + 31 positions past the
+wave's first query.  For them the NaN dims may be NaN or match, and every
+other dim must match."""
 import numpy as np
 import pytest
 
@@ -112,7 +115,7 @@ def test_prefill_special_values(orc, S, N):
     assert np.array_equal(np.isnan(f32(want)), expected_nan_rows(q_abs, k_pos, v_pos))
     exposed = np.zeros_like(want, dtype=bool)
     G = HQ // HKV
-    near = (q_abs < v_pos) & (q_abs >= v_pos - 31)
+    near = (q_abs < v_pos) & (q_abs >= v_pos - 46)
     for d in V_NAN_DIMS:
         exposed[V_NAN_HEAD * G:(V_NAN_HEAD + 1) * G, near, d] = True
     n = check(got, want, exposed, f"prefill S{S} N{N}")
