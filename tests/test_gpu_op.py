@@ -87,6 +87,16 @@ def test_op_config3_decode_with_append(orc):
             step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 5 + i, f"config3, one split, step {i}")
     assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0)), "K pages"
     assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1)), "V pages"
+    # split workgroups reading 4 kv heads each (the long-context plan, forced
+    # here): the wave of each head that reads the last page writes that
+    # head's appended token
+    with paged.decode_tuned(0, "kernel", 4):
+        for i in range(3):
+            step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 15 + i, f"config3, 4 kv heads per workgroup, step {i}")
+        with paged.decode_tuned(7, "kernel", 4):
+            step(mgr, ref, 0, Hq, Hkv, 1, D, seed + 19, "config3, 4 kv heads per workgroup, 7 pages per split")
+    assert np.array_equal(mgr.read_pool(0, 0), ref.pool_array(0, 0)), "K pages (4 heads)"
+    assert np.array_equal(mgr.read_pool(0, 1), ref.pool_array(0, 1)), "V pages (4 heads)"
     mgr.close()
 
 
