@@ -9,12 +9,12 @@
 // HPW kv heads (1, or 4 for long page ranges) and a contiguous range of
 // pages; the W / HPW waves of each head take its pages round-robin.
 // The kv head is the fastest grid index: the dispatcher deals workgroups to the
-// 8 XCDs round-robin, so with 8 kv heads every split of head h (and, with the
-// same order in the merge grid, that head's merge) runs on XCD h.  8 waves
-// serve ranges of up to kWideMaxPps pages at D = 128 (config 3's 32 and config
-// 5's 64-65): each wave then owns half the pages of a 4-wave form, so a split
-// finishes in fewer dependent memory round trips.  Longer ranges, and D = 256,
-// keep 4 waves.  The rows of the kv head -- its (query, GQA q-head) pairs, at
+// 8 XCDs round-robin, so with 8 kv heads and one head per workgroup every
+// split of head h (and, with the same order in the merge grid, that head's
+// merge) runs on XCD h.  8 waves serve ranges of up to kWideMaxPps pages at
+// D = 128 (config 3's 17) and every 4-head workgroup: each wave then owns half
+// the pages of a 4-wave form, so a split finishes in fewer dependent memory
+// round trips.  Longer one-head ranges, and D = 256, keep 4 waves.  The rows of the kv head -- its (query, GQA q-head) pairs, at
 // most 16 -- are the 16 columns of the MFMA tiles, so K/V are read once for all
 // of them.
 //
