@@ -13,14 +13,16 @@ held to the attention tolerance (max-abs <= 2^-7 max|ref|, rel-L2 <= 1e-2).
 A NaN score (NaN in K) poisons exactly the queries whose window holds the
 key in both: the reference's std::fmax keeps m and exp(NaN - m) feeds l and
 o, the kernels' masked scores are -inf before the exponent.  A NaN in V is
-different in the prefill kernel: the keys of a diagonal tile past a query's
-limit meet a zero probability in the P.V matrix product, and 0 x NaN is
-NaN, where the reference never visits those keys.  The queries so exposed
-sit at most 46 positions before the row: a wave of 16 queries multiplies
-the whole 32-key half it processes, and it processes a half that starts
-before its last query, so the key can lie up to 15 + 31 positions past the
-wave's first query.  For them the NaN dims may be NaN or match, and every
-other dim must match."""
+different: the keys past a query's limit that the kernels still multiply
+meet a zero probability in the P.V matrix product, and 0 x NaN is NaN,
+where the reference never visits those keys.  In the prefill kernel the
+queries so exposed sit at most 46 positions before the row: a wave of 16
+queries multiplies the whole 32-key half it processes, and it processes a
+half that starts before its last query, so the key can lie up to 15 + 31
+positions past the wave's first query.  In the decode kernel they are the
+query chunk's own queries before the row (a row inside the chunk; all rows
+of a kv head share the V operand).  For them the NaN dims may be NaN or
+match, and every other dim must match."""
 import numpy as np
 import pytest
 
@@ -87,19 +89,29 @@ def expected_nan_rows(q_abs, k_pos, v_pos):
     return m
 
 
-@pytest.mark.parametrize("S,pps", [(1, None), (1, 4), (3, None)])
-def test_decode_special_values(orc, S, pps):
+@pytest.mark.parametrize("S,pps,k_pos,v_pos", [(1, None, 600, 517), (1, 4, 600, 517), (3, None, 600, 517),
+                                               (3, None, 999, 998), (8, 3, 996, 994)])
+def test_decode_special_values(orc, S, pps, k_pos, v_pos):
+    """The planted rows either precede the whole query chunk, so every query
+    sees them, or sit inside it.  A NaN K row inside the chunk stays exact (its
+    score is masked to -inf before the exponent).  A NaN V row inside it also
+    meets the zero probabilities of the chunk's earlier queries in the P.V
+    MFMA, which every row of the kv head shares: those queries (q_abs < v_pos)
+    are the exposed set, and no other output may differ."""
     N = 1000
-    ctx = Context(orc, HKV, D, (N + 15) // 16 + 4, N, 8100 + S)
-    k_pos, v_pos = 600, 517
+    ctx = Context(orc, HKV, D, (N + 15) // 16 + 4, N, 8100 + S + v_pos)
     plant(ctx, k_pos, v_pos)
     q = synth.normal_bf16(8200 + S, (HQ, S, D))
     got, _ = ctx.decode(q, pps=pps)
     want = ctx.oracle(q)
     q_abs = np.arange(N - S, N)
     assert np.array_equal(np.isnan(f32(want)), expected_nan_rows(q_abs, k_pos, v_pos))
-    # the decode rows all sit past both planted rows: no query is exposed
-    check(got, want, np.zeros_like(want, dtype=bool), f"decode S{S} pps{pps}")
+    exposed = np.zeros_like(want, dtype=bool)
+    G = HQ // HKV
+    for d in V_NAN_DIMS:
+        exposed[V_NAN_HEAD * G:(V_NAN_HEAD + 1) * G, q_abs < v_pos, d] = True
+    n = check(got, want, exposed, f"decode S{S} pps{pps} k{k_pos} v{v_pos}")
+    print(f"[decode S{S} v{v_pos}] {n} outputs NaN through 0 x NaN products (reference finite)", flush=True)
     ctx.close()
 
 
