@@ -150,6 +150,12 @@ struct Elem<false> {
     }
     // an output element as the reference's from_f32_rt stores it
     static __device__ __forceinline__ uint32_t out(float f) { return f32_to_bf16_ref(f); }
+    static __device__ __forceinline__ float lo(uint32_t w) { return bf16_lo(w); }
+    static __device__ __forceinline__ float hi(uint32_t w) { return bf16_hi(w); }
+    // either element of a packed pair is NaN or infinite
+    static __device__ __forceinline__ bool nonfinite2(uint32_t w) {
+        return (w & 0x7F80u) == 0x7F80u || (w & 0x7F800000u) == 0x7F800000u;
+    }
 };
 template <>
 struct Elem<true> {
@@ -165,6 +171,13 @@ struct Elem<true> {
         return __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(lo), static_cast<_Float16>(hi)});
     }
     static __device__ __forceinline__ uint32_t out(float f) { return f32_to_f16_ref(f); }
+    static __device__ __forceinline__ float lo(uint32_t w) { return float(__builtin_bit_cast(_Float16, uint16_t(w))); }
+    static __device__ __forceinline__ float hi(uint32_t w) {
+        return float(__builtin_bit_cast(_Float16, uint16_t(w >> 16)));
+    }
+    static __device__ __forceinline__ bool nonfinite2(uint32_t w) {
+        return (w & 0x7C00u) == 0x7C00u || (w & 0x7C000000u) == 0x7C000000u;
+    }
 };
 
 // Every 64-byte line of the kernel's argument block requested at once, at

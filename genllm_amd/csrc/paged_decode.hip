@@ -430,8 +430,28 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Keys from chunk_from on are the query chunk's own (S > 1, causal): some
+    // rows may not see them.  Every row of the kv head multiplies every key of
+    // the page in the P.V MFMA, with a zero probability where it may not see
+    // it, and 0 x NaN is NaN: a NaN or infinite V row of such a key would reach
+    // rows the reference never lets it reach.  A page holding one leaves those
+    // keys out of the MFMA and adds them per row, over the rows that see them.
+    const int chunk_from = p.causal && S > 1 ? n_cached - S + 1 : n_cached;
     auto compute_page = [&](int j, const PageRegs<D>& pr, bool special) {
         const int tok0 = page_of(j) * kPage + 4 * g;  // this lane's 4 keys: tok0 .. tok0+3
+        bool split_v = false;  // wave-uniform
+        if (special && chunk_from < n_cached) {
+            bool bad = false;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int hh = 0; hh < VH; ++hh) {
+                    const uint4 u = pr.v[i][hh];
+                    const bool nf = E::nonfinite2(u.x) | E::nonfinite2(u.y) | E::nonfinite2(u.z) | E::nonfinite2(u.w);
+                    bad |= nf && tok0 + i >= chunk_from && tok0 + i < n_cached;
+                }
+            split_v = __any(bad);
+        }
         // V^T into LDS first (its latency hides behind the S^T MFMAs)
 #pragma unroll
         for (int hh = 0; hh < VH; ++hh) {
@@ -439,7 +459,8 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 v[i] = pr.v[i][hh];
-                if (special && tok0 + i >= n_cached) v[i] = make_uint4(0, 0, 0, 0);  // unfilled slots
+                // unfilled slots, and the chunk's keys when they are added per row
+                if (special && (tok0 + i >= n_cached || (split_v && tok0 + i >= chunk_from))) v[i] = make_uint4(0, 0, 0, 0);
             }
             const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w}, {v[1].x, v[1].y, v[1].z, v[1].w},
                                       {v[2].x, v[2].y, v[2].z, v[2].w}, {v[3].x, v[3].y, v[3].z, v[3].w}};
@@ -498,6 +519,29 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
             acc[db] = E::mma16(a, pb, acc[db]);
         }
         __builtin_amdgcn_wave_barrier();
+        if (split_v) {
+            // the chunk's keys of this page, per row: lane (row n16, g) adds key t
+            // to its dims 16 db + 4g .. + 3 when the row sees t
+            const int pg0 = page_of(j) * kPage;
+            const int t_hi = min(pg0 + kPage, n_cached);
+            for (int t = max(pg0, chunk_from); t < t_hi; ++t) {
+                const int kk = t - pg0, ki = kk & 3;
+                const float sel = ki == 0 ? pw[0] : ki == 1 ? pw[1] : ki == 2 ? pw[2] : pw[3];
+                const float pk = __shfl(sel, n16 + 16 * (kk >> 2));  // P[row][t]
+                const uint16_t* vrow = fused && t >= new_from
+                                           ? p.v_new + h * p.new_head_stride + int64_t(t - new_from) * p.new_tok_stride
+                                           : p.v_pool + int64_t(pr.vid) * p.page_elems + int64_t(kk) * p.kv_row + h * D;
+                if (t > qabs) continue;  // per lane: this row does not see t
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const uint2 u = *reinterpret_cast<const uint2*>(vrow + 16 * db + 4 * g);
+                    acc[db][0] = __builtin_fmaf(pk, E::lo(u.x), acc[db][0]);
+                    acc[db][1] = __builtin_fmaf(pk, E::hi(u.x), acc[db][1]);
+                    acc[db][2] = __builtin_fmaf(pk, E::lo(u.y), acc[db][2]);
+                    acc[db][3] = __builtin_fmaf(pk, E::hi(u.y), acc[db][3]);
+                }
+            }
+        }
     };
 
     // pages are loaded in increasing j, each once: the wave moves to id block

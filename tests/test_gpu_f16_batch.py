@@ -141,6 +141,40 @@ def test_f16_special_values(orc):
     mgr.close()
 
 
+def test_f16_decode_chunk_special_values(orc):
+    """A 3-query decode chunk on fp16 layers whose own second key holds a NaN
+    and a +inf in one V row (kv head 1): the chunk's first query does not see
+    that key and stays finite, as in the reference; the two others get the
+    reference's non-finite outputs (float16_t turns the NaN into an infinity;
+    bit-equal up to the sign); every finite output is held to the fp16
+    attention tolerance."""
+    Hq, Hkv, D, pool, P, S = 4, 2, 128, 8, 30, 3
+    G = Hq // Hkv
+    mgr, ref = make(orc, Hkv, D, pool, 91, orc.F16)
+    step(orc, mgr, ref, Hq, Hkv, P, D, 9100, "f16 prompt")
+    q = synth.normal_f16(9200, (1, Hq, S, D))
+    k = synth.normal_f16(9201, (1, Hkv, S, D))
+    v = synth.normal_f16(9202, (1, Hkv, S, D)).copy()
+    v[0, 1, 1, 5] = np.float16(np.nan).view(np.uint16)
+    v[0, 1, 1, 7] = np.float16(np.inf).view(np.uint16)
+    out = torch.zeros((1, Hq, S, D), dtype=torch.float16, device="cuda")
+    paged.paged_attention(mgr, 0, paged.to_device_f16(q), paged.to_device_f16(k), paged.to_device_f16(v), out, G,
+                          scale_for(D))
+    torch.cuda.synchronize()
+    want, rc = ref.paged_attention(0, q, k, v, G, scale_for(D), True, dtype=orc.F16)
+    assert rc == 0
+    got = paged.to_host_bits(out)
+    w_nf = ~np.isfinite(want.view(np.float16))
+    g_nf = ~np.isfinite(got.view(np.float16))
+    assert np.array_equal(w_nf, g_nf), f"non-finite outputs at {np.argwhere(w_nf != g_nf)[:6]}"
+    assert np.array_equal(got[w_nf] & 0x7FFF, want[w_nf] & 0x7FFF)
+    heads = slice(G, 2 * G)  # the q heads of kv head 1
+    assert not w_nf[0, heads, 0].any() and w_nf[0, heads, 1:][..., [5, 7]].all() and w_nf.sum() == 2 * 2 * 2
+    assert_attn_close_f16(np.where(w_nf, 0, got).astype(np.uint16), np.where(w_nf, 0, want).astype(np.uint16),
+                          "f16 decode chunk, finite outputs")
+    mgr.close()
+
+
 @pytest.mark.parametrize("f16", [False, True])
 def test_batch2_entries_share_the_cache(orc, f16):
     """batch = 2 through the op: a 40-token prefill chunk, then decode steps;
