@@ -91,13 +91,16 @@ def test_decode_shapes(orc, Hq, Hkv, N):
     ctx.close()
 
 
-def test_decode_very_long_context(orc):
-    """131,073 cached keys (8,193 pages of a shuffled 8,200-page pool, the
-    last page holding one key): the default plan gives 257 pages per split,
-    the 4-wave form with 32+ page ids per wave."""
-    N, pool = 131073, 8200
-    ctx = Context(orc, 8, 128, pool, N, 131000, nan_tail=True)
-    q = synth.normal_bf16(131001, (32, 1, 128))
+@pytest.mark.parametrize("N", [131073, 262145])
+def test_decode_very_long_context(orc, N):
+    """131,073 and 262,145 cached keys (8,193 and 16,385 pages of a shuffled
+    pool, the last page holding one key).  The default plan reads 4 kv heads
+    per split workgroup: 65 pages per split over 127 splits (33 pages per
+    wave), then 129 pages per split over 128 splits (65 pages per wave, two
+    blocks of page ids)."""
+    pool = (N + 15) // 16 + 7
+    ctx = Context(orc, 8, 128, pool, N, N - 73, nan_tail=True)
+    q = synth.normal_bf16(N - 72, (32, 1, 128))
     got, _ = ctx.decode(q)
     assert_attn_close(got, ctx.oracle(q), f"N{N}")
     ctx.close()
