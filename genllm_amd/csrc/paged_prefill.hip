@@ -6,7 +6,8 @@
 // kv head = q head / groups (:158).
 //
 // Grid: query tiles of 64 rows x Hq workgroups of 8 waves: the long half of
-// the query tiles from the last down, then the short half from the first up.
+// the query tiles from the last down, then the short half from the first up;
+// q heads placed so that those of one kv head share an XCD.
 // Wave w = qb + 4 kh owns query block qb (16 queries) of the tile and key
 // half kh (32 keys) of every key tile of 64 tokens (4 pages), so the two key
 // halves of a query block share a SIMD (waves w and w + 4; measured 30.9
@@ -127,7 +128,13 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
     const int n16 = lane & 15, g = lane >> 4;
     const int n_qt = (p.S + QT - 1) / QT;
     const int rank = int(blockIdx.x) / p.Hq;
-    const int hq = int(blockIdx.x) - rank * p.Hq;
+    const int slot = int(blockIdx.x) - rank * p.Hq;
+    // Workgroup i runs on XCD i % 8.  With Hq a multiple of 8, slot 8j + x
+    // takes q head x Hq/8 + j, so XCD x holds q heads [x Hq/8, (x+1) Hq/8) and
+    // the q heads of one kv head read its tiles through one L2 (config 4:
+    // FETCH_SIZE 16.2 against 24.2 MiB per launch, the algorithmic q and K/V
+    // bytes against 1.5x; 30.32-30.41 against 30.44-30.56 us, A/B on one box)
+    const int hq = (p.Hq & 7) == 0 ? (slot & 7) * (p.Hq >> 3) + (slot >> 3) : slot;
     // the first half of the grid runs the query tiles with the most keys, from
     // the last tile down; the second half the others from the first tile up,
     // so that workgroups i and i + half the grid -- the two a CU holds when
