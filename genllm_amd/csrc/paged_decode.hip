@@ -701,7 +701,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(const int32_t* k_i
 // with the same rule
 //   M = max M_w, L = sum L_w 2^(M_w - M), O = sum O_w 2^(M_w - M), out = O / L.
 // MW is 4, or 8 above 4 * kMergeU splits (measured: 8 waves cost about 0.4 us
-// at 31-32 splits and save 0.6 us at 103).  Blocks of 64 dims rather than one
+// at 31-32 splits and save 0.6 us at 103; 2 waves at 31 splits cost 0.3 us).  Blocks of 64 dims rather than one
 // workgroup per row (D dims) spread a row's partials over D / 64 CUs; on one
 // box, 128-dim blocks against 64: Qwen3.5 (D = 256, 103 splits) 12.8 -> 12.3
 // us per decode, config 3 13.1 -> 12.9 us (whole rows measured 14.2 us on the
