@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from genllm_amd import synth
-from helpers import assert_attn_close
+from helpers import assert_attn_close, f32
 from test_gpu_decode import Context
 from test_gpu_prefill import run_prefill
 
@@ -57,4 +57,44 @@ def test_prefill_random_shapes(orc, i):
     q = synth.normal_bf16(9600 + i, (Hkv * G, S, D))
     got = run_prefill(ctx, q, causal)
     assert_attn_close(got, ctx.oracle(q, causal), f"prefill case {i}: D{D} Hkv{Hkv} G{G} S{S} N{N} causal{causal}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_decode_random_special_values(orc, i):
+    """Seeded multi-query decode chunks with a NaN and a +inf planted in V rows
+    and a NaN in a K row of the chunk's own keys (random kv head, dims and
+    positions): the set of NaN and infinite outputs equals the oracle's (the
+    values up to the sign of a NaN), and every finite output is held to the
+    attention tolerance."""
+    r = np.random.default_rng(0x5EC0 + i)
+    D = int(r.choice([128, 256]))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    S = int(r.choice([2, 3, 4, 8]))
+    G = int(r.choice([g for g in (1, 2, 4, 8) if g * S <= 16]))
+    N = int(r.integers(S + 20, 2000))
+    pool = (N + 15) // 16 + 2
+    ctx = Context(orc, Hkv, D, pool, N, 9700 + i, nan_tail=True)
+    kt, vt = ctx.ref.page_table(0)
+    kp, vp = ctx.ref.pool_array(0, 0), ctx.ref.pool_array(0, 1)
+    chunk = np.arange(N - S, N)
+    h = int(r.integers(Hkv))
+    t_nan, t_inf, t_k = (int(x) for x in r.choice(chunk, 3))
+    d_nan, d_inf, d_k = (int(x) for x in r.integers(D, size=3))
+    vp[vt[t_nan // 16], t_nan % 16, h, d_nan] = 0x7FC0
+    vp[vt[t_inf // 16], t_inf % 16, h, d_inf] = 0x7F80
+    kp[kt[t_k // 16], t_k % 16, h, d_k] = 0xFFC0
+    ctx.mgr.write_pool(0, 0, np.ascontiguousarray(kp))
+    ctx.mgr.write_pool(0, 1, np.ascontiguousarray(vp))
+    q = synth.normal_bf16(9800 + i, (Hkv * G, S, D))
+    got, _ = ctx.decode(q)
+    want = ctx.oracle(q)
+    label = f"special case {i}: D{D} Hkv{Hkv} G{G} S{S} N{N} v-nan {t_nan} v-inf {t_inf} k-nan {t_k}"
+    gf, wf = f32(got), f32(want)
+    assert np.array_equal(np.isnan(gf), np.isnan(wf)), label + ": NaN outputs differ"
+    assert np.array_equal(np.isinf(gf), np.isinf(wf)), label + ": infinite outputs differ"
+    nf = ~np.isfinite(wf)
+    assert np.array_equal(got[nf] & 0x7FFF, want[nf] & 0x7FFF), label + ": non-finite bits"
+    assert nf.any(), label + ": nothing planted reached an output"
+    assert_attn_close(np.where(nf, 0, got).astype(np.uint16), np.where(nf, 0, want).astype(np.uint16), label)
     ctx.close()
