@@ -108,6 +108,74 @@ __device__ __forceinline__ void tile_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
+// The key half kh (keys KT t + KH kh .. + KH - 1 of every key tile t) below
+// wave_end, for query q0 + n16 (lane n16 + 16 g), formed the reference's way:
+// per query over the keys it sees, in fp32, one key after another.  res: the
+// O^T values of the lane's dims 16 db + 4 g + i, then m (log2 units) and l
+// (the row's, in lane g = 0; 0 elsewhere, as the hand-over adds the four
+// lanes).  Called only by waves whose tiled state came out NaN or infinite.
+template <int D, bool F16>
+__device__ __forceinline__ void prefill_exact_half(const AttnParams& p, int hq, int q0, int kh, int wave_end,
+                                                   int n_tiles, float* res) {
+    using E = Elem<F16>;
+    constexpr int KS = D / 32, DB = D / 16, KH = KT / 2;
+    const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
+    const int n_cached = p.n_cached, qabs0 = p.n_cached - p.S;
+    const int lim = p.causal ? min(qabs0 + q0 + n16 + 1, n_cached) : n_cached;
+    const int hkv = hq / p.G;
+    const int64_t head_off = int64_t(hkv) * (p.kv_head_stride ? p.kv_head_stride : D);
+    const bool paged = p.k_ids != nullptr;
+    const uint16_t* const qrow = p.q + int64_t(hq) * p.q_head_stride + int64_t(min(q0 + n16, p.S - 1)) * p.q_tok_stride;
+    const float c = fmaxf(p.scale_log2, __FLT_MIN__);
+    float m = -INFINITY, l = 0.0f;
+    f32x4_t acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < n_tiles; ++t) {
+        for (int j = 0; j < KH; ++j) {
+            const int tok = t * KT + KH * kh + j;
+            if (tok >= wave_end) break;  // wave-uniform
+            const int64_t in_page = int64_t(tok % kPage) * p.kv_row;
+            const int64_t krow = paged ? int64_t(p.k_ids[tok / kPage]) * p.page_elems + in_page : int64_t(tok) * p.kv_row;
+            const int64_t vrow = paged ? int64_t(p.v_ids[tok / kPage]) * p.page_elems + in_page : int64_t(tok) * p.kv_row;
+            float sp = 0.0f;  // this lane's dims 32 ks + 8 g .. + 7, then the row's four lanes
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint4 qq = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
+                const uint4 kk = *reinterpret_cast<const uint4*>(p.k_pool + head_off + krow + 32 * ks + 8 * g);
+                const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+                for (int w2 = 0; w2 < 4; ++w2) {
+                    sp = __builtin_fmaf(E::lo(qw[w2]), E::lo(kw[w2]), sp);
+                    sp = __builtin_fmaf(E::hi(qw[w2]), E::hi(kw[w2]), sp);
+                }
+            }
+            sp += __shfl_xor(sp, 16);
+            sp += __shfl_xor(sp, 32);
+            const bool vis = tok < lim;
+            const float x = sp * c;
+            const float mn = vis ? __builtin_fmaxf(m, x) : m;
+            const float alpha = m == -INFINITY ? 0.0f : exp2_fast(m - mn);
+            const float pk = exp2_fast(x - mn);
+            l = vis ? __builtin_fmaf(l, alpha, pk) : l;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const uint2 u = *reinterpret_cast<const uint2*>(p.v_pool + head_off + vrow + 16 * db + 4 * g);
+                const float v4[4] = {E::lo(u.x), E::hi(u.x), E::lo(u.y), E::hi(u.y)};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[db][i] = vis ? __builtin_fmaf(pk, v4[i], acc[db][i] * alpha) : acc[db][i];
+            }
+            m = mn;
+        }
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) res[4 * db + i] = acc[db][i];
+    res[4 * DB] = m;
+    res[4 * DB + 1] = g == 0 ? l : 0.0f;
+}
+
 template <int D, bool F16>
 __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
     using E = Elem<F16>;
@@ -352,6 +420,33 @@ __device__ __forceinline__ void prefill_tiles(const AttnParams& p) {
         step(t + 1, buf1, buf0);
     }
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the trailing (empty) loads have landed: LDS is free
+
+    // Keys of a masked half that a query may not see meet a zero probability
+    // in the P.V MFMA, and 0 x NaN is NaN: a NaN or infinite V row there would
+    // reach queries the reference never lets it reach.  A wave whose state
+    // came out NaN or infinite (only ever with such inputs) forms its key half
+    // again from the pools, in fp32, visiting for each query only the keys it
+    // sees, as the reference's loop does.  The check is one sum of the state
+    // (a NaN or an infinity in it makes the sum non-finite); measured at
+    // config 4, 30.85-30.93 against 30.65-30.80 us (A/B on one box, two passes;
+    // checking each value instead cost 0.3-0.4 us).
+    {
+        float tsum = l;  // NaN or infinite when any of the state is
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tsum += acc[db][i];
+        if (__any(!(fabsf(tsum) <= __FLT_MAX__))) {
+            float res[DB * 4 + 2];
+            prefill_exact_half<D, F16>(p, hq, q0, kh, wave_end, n_tiles, res);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[db][i] = res[4 * db + i];
+            m = res[4 * DB];
+            l = res[4 * DB + 1];
+        }
+    }
 
     // ---- merge the two key halves of each query block: the key-half-1 wave
     // stores (O^T, m, l) as [value][lane] floats, the key-half-0 wave combines

@@ -98,3 +98,43 @@ def test_decode_random_special_values(orc, i):
     assert nf.any(), label + ": nothing planted reached an output"
     assert_attn_close(np.where(nf, 0, got).astype(np.uint16), np.where(nf, 0, want).astype(np.uint16), label)
     ctx.close()
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_prefill_random_special_values(orc, i):
+    """Seeded prefill chunks with a NaN and a +inf planted in V rows and a NaN
+    in a K row of the chunk's own keys (random kv head, dims and positions,
+    so that each row is past some queries' causal limit): the set of NaN and
+    infinite outputs equals the oracle's (the values up to the sign of a NaN),
+    and every finite output is held to the attention tolerance."""
+    r = np.random.default_rng(0x5ED0 + i)
+    D = int(r.choice([128, 256]))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 4]))
+    S = int(r.integers(40, 300))
+    N = S + int(r.integers(0, 300))
+    pool = (N + 15) // 16 + 2
+    ctx = Context(orc, Hkv, D, pool, N, 9900 + i, nan_tail=True)
+    kt, vt = ctx.ref.page_table(0)
+    kp, vp = ctx.ref.pool_array(0, 0), ctx.ref.pool_array(0, 1)
+    chunk = np.arange(N - S, N)
+    h = int(r.integers(Hkv))
+    t_nan, t_inf, t_k = (int(x) for x in r.choice(chunk, 3))
+    d_nan, d_inf, d_k = (int(x) for x in r.integers(D, size=3))
+    vp[vt[t_nan // 16], t_nan % 16, h, d_nan] = 0x7FC0
+    vp[vt[t_inf // 16], t_inf % 16, h, d_inf] = 0x7F80
+    kp[kt[t_k // 16], t_k % 16, h, d_k] = 0xFFC0
+    ctx.mgr.write_pool(0, 0, np.ascontiguousarray(kp))
+    ctx.mgr.write_pool(0, 1, np.ascontiguousarray(vp))
+    q = synth.normal_bf16(9950 + i, (Hkv * G, S, D))
+    got = run_prefill(ctx, q, True)
+    want = ctx.oracle(q, True)
+    label = f"prefill special case {i}: D{D} Hkv{Hkv} G{G} S{S} N{N} v-nan {t_nan} v-inf {t_inf} k-nan {t_k}"
+    gf, wf = f32(got), f32(want)
+    assert np.array_equal(np.isnan(gf), np.isnan(wf)), label + ": NaN outputs differ"
+    assert np.array_equal(np.isinf(gf), np.isinf(wf)), label + ": infinite outputs differ"
+    nf = ~np.isfinite(wf)
+    assert np.array_equal(got[nf] & 0x7FFF, want[nf] & 0x7FFF), label + ": non-finite bits"
+    assert nf.any(), label + ": nothing planted reached an output"
+    assert_attn_close(np.where(nf, 0, got).astype(np.uint16), np.where(nf, 0, want).astype(np.uint16), label)
+    ctx.close()
