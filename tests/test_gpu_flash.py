@@ -139,3 +139,54 @@ def test_flash_rejects_bad_shapes():
     k = torch.zeros((1, 4, 8, 128), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(GenllmError):  # 6 q heads cannot map onto 4 kv heads with groups 2
         paged.flash_attention(q, k, k, torch.empty_like(q), 2, 0.125)
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_flash_special_values_vs_oracle(orc, D):
+    """Non-paged causal attention with a NaN and a +inf in V rows and a NaN in
+    a K row, each past some queries' causal limit.  The reference's two
+    backends differ here: its CUDA kernel skips masked keys
+    (src/backend/cuda/attention.cu:278-279), so such a V row reaches only the
+    queries that see it, while its CPU loop (attention.cpp:39-121) gives
+    masked keys a zero weight and 0 x NaN, 0 x inf are NaN for every earlier
+    query.  The GPU op follows the CUDA kernel, exactly: outputs of queries
+    that see a planted row are the oracle's, those of queries that do not are
+    the oracle's with the planted V values zeroed (a masked key adds
+    nothing); NaN and infinite outputs in the same places (values up to the
+    sign of a NaN), finite outputs within the tolerance.  The CPU loop's
+    non-finite set contains the GPU's."""
+    import torch
+
+    from genllm_amd import paged, synth
+    from helpers import f32
+
+    B, Hq, Hkv, S = 2, 8, 2, 150
+    scale = 1.0 / np.sqrt(D)
+    q, k, v = _inputs(synth, 1700 + D, B, Hq, Hkv, S, D)
+    k, v = k.copy(), v.copy()
+    v0 = v.copy()
+    v[0, 1, 60, 7] = 0x7FC0   # NaN: batch 0, kv head 1 (q heads 4-7), key 60
+    v[1, 0, 100, 3] = 0x7F80  # +inf: batch 1, kv head 0 (q heads 0-3), key 100
+    k[1, 1, 120, 9] = 0xFFC0  # NaN score for key 120 of kv head 1 (q heads 4-7)
+    out = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    paged.flash_attention(paged.to_device_bf16(q), paged.to_device_bf16(k), paged.to_device_bf16(v), out,
+                          Hq // Hkv, scale, True)
+    torch.cuda.synchronize()
+    cpu = orc.flash_attention(q, k, v, Hq // Hkv, scale, True)
+    zeroed = orc.flash_attention(q, k, v0, Hq // Hkv, scale, True)
+    sees = np.zeros(cpu.shape, dtype=bool)
+    sees[0, 4:8, 60:] = True
+    sees[1, 0:4, 100:] = True
+    want = np.where(sees, cpu, zeroed).astype(np.uint16)
+    got = paged.to_host_bits(out)
+    gf, wf = f32(got), f32(want)
+    assert np.array_equal(np.isnan(gf), np.isnan(wf)), "NaN outputs differ"
+    assert np.array_equal(np.isinf(gf), np.isinf(wf)), "infinite outputs differ"
+    nf = ~np.isfinite(wf)
+    assert nf[0, 4:8, 60:, 7].all() and not nf[0, 4:8, :60].any(), "the NaN V row reaches queries 60.. only"
+    assert np.isposinf(wf[1, 0:4, 100:, 3]).all() and not nf[1, 0:4, :100].any(), "+inf reaches queries 100.."
+    assert np.isnan(wf[1, 4:8, 120:]).all() and not nf[1, 4:8, :120].any(), "the NaN score: queries 120.."
+    assert np.array_equal(got[nf] & 0x7FFF, want[nf] & 0x7FFF)
+    assert (~np.isfinite(f32(cpu)))[nf].all(), "the CPU loop's non-finite set contains the GPU's"
+    assert_attn_close(np.where(nf, 0, got).astype(np.uint16), np.where(nf, 0, want).astype(np.uint16),
+                      f"flash D{D} special values, finite outputs")
