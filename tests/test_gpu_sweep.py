@@ -138,3 +138,39 @@ def test_prefill_random_special_values(orc, i):
     assert nf.any(), label + ": nothing planted reached an output"
     assert_attn_close(np.where(nf, 0, got).astype(np.uint16), np.where(nf, 0, want).astype(np.uint16), label)
     ctx.close()
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_decode_random_tuned(orc, i):
+    """Seeded decode shapes under a random decode tuning (genllm_decode_tuning):
+    the merge in a kernel or in the last split workgroup, 1 or 4 kv heads per
+    split workgroup, and forced split sizes from one page up."""
+    r = np.random.default_rng(0x7E40 + i)
+    D = int(r.choice([128, 256]))
+    Hkv = int(r.choice([2, 4, 8]))
+    S = int(r.choice([1, 1, 2, 4]))
+    G = int(r.choice([g for g in (1, 2, 4, 8) if g * S <= 16]))
+    N = int(r.integers(S, 5000))
+    merge = str(r.choice(["kernel", "fused"]))
+    heads = int(r.choice([0, 1, 4])) if Hkv % 4 == 0 else int(r.choice([0, 1]))
+    pps = int(r.choice([0, 1, 3, 17, 64]))
+    pool = (N + 15) // 16 + 1 + i % 3
+    ctx = Context(orc, Hkv, D, pool, N, 9200 + i, nan_tail=True)
+    q = synth.normal_bf16(9300 + i, (Hkv * G, S, D))
+    got, _ = ctx.decode(q, pps=pps or None, merge=merge, heads=heads)
+    assert_attn_close(got, ctx.oracle(q), f"tuned case {i}: D{D} Hkv{Hkv} G{G} S{S} N{N} {merge} heads{heads} pps{pps}")
+    ctx.close()
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_prefill_random_token_layout(orc, i):
+    """Seeded prefill chunks with q and out token-major ([S][Hq][D], the
+    layout a fused projection writes), against the head-major oracle."""
+    D, Hkv, G, S, N, causal = prefill_case(100 + i)
+    pool = (N + 15) // 16 + 1 + i % 4
+    ctx = Context(orc, Hkv, D, pool, N, 9400 + i, nan_tail=True)
+    q = synth.normal_bf16(9450 + i, (Hkv * G, S, D))
+    got = run_prefill(ctx, np.ascontiguousarray(q.transpose(1, 0, 2)), causal, q_layout="token")
+    assert_attn_close(np.ascontiguousarray(got.transpose(1, 0, 2)), ctx.oracle(q, causal),
+                      f"token-layout prefill {i}: D{D} Hkv{Hkv} G{G} S{S} N{N} causal{causal}")
+    ctx.close()
