@@ -814,6 +814,14 @@ def measure_counters():
         timed = {k: sorted(v)[-n:] for k, v in kernels.items()}
         per_kernel = {re.search(r"paged_decode\w*<[^>]*>", k).group(0):
                       round(statistics.mean(e - b for b, e in v) / 1e3, 3) for k, v in timed.items()}
+
+        def spread(durs):  # nearest-rank p10, median, p90 of the traced durations, us
+            s = sorted(durs)
+            return {q: round(s[min(len(s) - 1, int(round(f * (len(s) - 1))))] / 1e3, 3)
+                    for q, f in (("p10", 0.1), ("median", 0.5), ("p90", 0.9))}
+
+        per_kernel_spread = {re.search(r"paged_decode\w*<[^>]*>", k).group(0): spread([e - b for b, e in v])
+                             for k, v in timed.items()}
         t0 = min(v[0][0] for v in timed.values())
         t1 = max(v[-1][1] for v in timed.values())
         # the traced process also timed the same launches with HIP events
@@ -822,7 +830,8 @@ def measure_counters():
             for line in log:
                 if line.startswith("{") and "events_us_per_launch" in line:
                     ev = json.loads(line)["events_us_per_launch"]
-        res["kernel_trace"] = {"mean_us": per_kernel, "sum_us": round(sum(per_kernel.values()), 3),
+        res["kernel_trace"] = {"mean_us": per_kernel, "p10_median_p90_us": per_kernel_spread,
+                               "sum_us": round(sum(per_kernel.values()), 3),
                                "timeline_us_per_decode": round((t1 - t0) / 1e3 / n, 3), "decodes": n,
                                "events_us_per_decode_traced": ev,
                                "note": "durations under rocprofv3 --kernel-trace; events_us_per_decode_traced is "
