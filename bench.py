@@ -358,7 +358,7 @@ def f16_config3(args, np, torch, paged, synth, call):
 def append_cfg2(np, torch, paged, synth, call):
     S, Hkv, D, pool = 4096, 8, 128, 1024
     seed = synth.config_seed(2)
-    copies = 8
+    copies = 16  # 256 MB of k/v inputs: the 256 MB MALL cannot serve them between uses
     m2 = paged.PagedAttentionManager(copies * (2 * pool * PAGE * Hkv * D * 2 + 8 * pool + 4096) + (1 << 20))
     ks, vs = [], []
     for c in range(copies):
