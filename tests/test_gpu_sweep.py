@@ -174,3 +174,30 @@ def test_prefill_random_token_layout(orc, i):
     assert_attn_close(np.ascontiguousarray(got.transpose(1, 0, 2)), ctx.oracle(q, causal),
                       f"token-layout prefill {i}: D{D} Hkv{Hkv} G{G} S{S} N{N} causal{causal}")
     ctx.close()
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_op_random_sequences(orc, i):
+    """Seeded sequences of op steps (genllm_paged_attention: append, then
+    attend) on one layer: prefill chunks and decode steps of random length,
+    batch 2 for short steps, fp16 or bf16 layers; every step's output, page
+    tables and cached count against the oracle op's."""
+    from test_gpu_f16_batch import make, step
+
+    r = np.random.default_rng(0x0B5E80 + i)
+    D = int(r.choice([128, 256]))
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 4]))
+    f16 = bool(r.random() < 0.5)
+    pool = int(r.integers(40, 120))
+    mgr, ref = make(orc, Hkv, D, pool, 51000 + 11 * i, orc.F16 if f16 else orc.BF16)
+    n = 0
+    for j in range(int(r.integers(2, 6))):
+        S = int(r.choice([1, 1, 2, 3, int(r.integers(4, 200))]))
+        batch = int(r.choice([1, 1, 2])) if S <= 4 else 1
+        if n + S > pool * 16 - 16:
+            break
+        step(orc, mgr, ref, Hkv * G, Hkv, S, D, 61000 + 97 * i + j,
+             f"sequence {i} step {j}: D{D} Hkv{Hkv} G{G} {'fp16' if f16 else 'bf16'} n{n} S{S} batch{batch}",
+             f16=f16, batch=batch)
+        n += S
